@@ -1,0 +1,264 @@
+"""Benchmark of the MI355X FP8 path (one JSON line on stdout).
+
+Headline (``value``): the W8A8 gate_up GEMM of config 1 at M=4096 beam rows
+(K=2048, N=12288, bf16 out) in TFLOP/s, one launch per step, with operands
+already resident in HBM and rotated over enough copies (> 512 MB) that no
+step is served from the 256 MB MALL.  ``extra`` carries the other kernels of
+the path at their configuration sizes (GB/s for the bandwidth-bound ones,
+TFLOP/s for GEMMs), each with its roofline fraction.  ``cpu_baseline`` times
+the reference's CPU torch path for the same GEMM on a bounded row sample.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--quick]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+import torch  # noqa: E402
+
+PEAK_FP8_TFLOPS = 5000.0  # MI355X dense fp8 MFMA
+PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
+MALL_DEFEAT_BYTES = 600 * 2**20
+
+
+def _timed(fn, steps: int, warmup: int) -> float:
+    """Average ms per call of ``fn(i)`` over ``steps`` calls, HIP events on the
+    current stream (the stream every kernel of the path is launched on)."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fn(i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def _copies(nbytes: int) -> int:
+    return max(2, math.ceil(MALL_DEFEAT_BYTES / max(1, nbytes)))
+
+
+def _gemm_case(dev, m, n, k, steps, warmup, seed, rotate=True):
+    from flashrec_amd.kernel.sglops import fp8_scaled_mm, per_token_quant_fp8
+    from flashrec_amd.layers.linear import quantize_weight_fp8
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    reps = _copies(m * k + n * k) if rotate else 1
+    acts, weights = [], []
+    for _ in range(reps):
+        x = torch.randn(m, k, device=dev, generator=g, dtype=torch.float32).to(torch.bfloat16)
+        w = (0.02 * torch.randn(n, k, device=dev, generator=g, dtype=torch.float32)).to(torch.bfloat16)
+        acts.append(per_token_quant_fp8(x))
+        q, s = quantize_weight_fp8(w)
+        weights.append((q.t(), s))
+        del x, w
+    out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+
+    def step(i):
+        qa, sa = acts[i % reps]
+        qw, sw = weights[i % reps]
+        fp8_scaled_mm(qa, qw, sa, sw, torch.bfloat16)
+
+    ms = _timed(step, steps, warmup)
+    del acts, weights, out
+    flops = 2.0 * m * n * k
+    return ms, flops / (ms * 1e-3) / 1e12
+
+
+def _bw_case(fn_factory, dev, steps, warmup, nbytes):
+    step, cleanup = fn_factory()
+    ms = _timed(step, steps, warmup)
+    cleanup()
+    return ms, nbytes / (ms * 1e-3) / 1e9
+
+
+def _rms_case(dev, m, h, rotate):
+    from flashrec_amd.kernel.rms_fp8 import rmsnorm_per_token_quant_fp8
+
+    nbytes = m * h * 2 + h * 2 + m * h + m * 4
+    reps = _copies(nbytes) if rotate else 1
+
+    def factory():
+        xs = [torch.randn(m, h, device=dev).to(torch.bfloat16) for _ in range(reps)]
+        gamma = (1 + 0.1 * torch.randn(h, device=dev)).to(torch.bfloat16)
+
+        def step(i):
+            rmsnorm_per_token_quant_fp8(xs[i % reps], gamma, 1e-6)
+
+        return step, lambda: xs.clear()
+
+    return factory, nbytes
+
+
+def _silu_case(dev, m, d, rotate):
+    from flashrec_amd.kernel.silu_fp8 import silu_and_mul_per_token_quant_fp8
+
+    nbytes = m * 2 * d * 2 + m * d + m * 4
+    reps = _copies(nbytes) if rotate else 1
+
+    def factory():
+        xs = [torch.randn(m, 2 * d, device=dev).to(torch.bfloat16) for _ in range(reps)]
+
+        def step(i):
+            silu_and_mul_per_token_quant_fp8(xs[i % reps])
+
+        return step, lambda: xs.clear()
+
+    return factory, nbytes
+
+
+def _rope_case(dev, t, hq, hk, d, slots, rotate):
+    from flashrec_amd.kernel.qk_rope_kv import fused_qk_norm_rope_store_fp8
+    from flashrec_amd.layers.rotary import build_cos_sin_cache
+
+    nbytes = t * hq * d * 2 * 2 + 2 * t * hk * d * 2 + 2 * t * hk * d + 2 * t * 8 + 2 * d * 2
+    reps = _copies(nbytes) if rotate else 1
+
+    def factory():
+        g = torch.Generator().manual_seed(3)
+        bufs = []
+        for _ in range(reps):
+            q = torch.randn(t, hq, d, device=dev).to(torch.bfloat16)
+            k = torch.randn(t, hk, d, device=dev).to(torch.bfloat16)
+            v = torch.randn(t, hk, d, device=dev).to(torch.bfloat16)
+            bufs.append((q, k, v))
+        per_req = max(1, t // 8)
+        prompt = torch.randint(64, 257, (8,), generator=g)
+        step_no = torch.randint(0, 5, (8,), generator=g)
+        pos = (prompt + step_no)[torch.clamp(torch.arange(t) // per_req, max=7)].to(dev)
+        loc = (torch.randperm(slots - 1, generator=g)[:t] + 1).to(dev)
+        cache = build_cos_sin_cache(d, 4096, 1e6).to(dev)
+        kc = torch.zeros(slots, hk, d, dtype=torch.float8_e4m3fn, device=dev)
+        vc = torch.zeros_like(kc)
+        w = torch.ones(d, dtype=torch.bfloat16, device=dev)
+
+        def step(i):
+            q, k, v = bufs[i % reps]
+            fused_qk_norm_rope_store_fp8(q, k, v, pos, loc, w, w, 1e-6, cache, kc, vc)
+
+        return step, lambda: bufs.clear()
+
+    return factory, nbytes
+
+
+def cpu_baseline(m_sample: int = 32, runs: int = 3):
+    """The reference's CPU torch path for the headline GEMM (torch._scaled_mm +
+    per-row/per-channel rescale, python/flashrec/kernel/sglops.py:111-139) on
+    ``m_sample`` rows of config 1; TFLOP/s."""
+    from oracle import inputs, ops
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(m_sample, 2048, generator=g).to(torch.bfloat16)
+    qa, sa = ops.per_token_quant_fp8(x)
+    qw, sw = ops.quantize_weight_fp8(inputs.config1_weight())
+    b = qw.t()
+    ops.fp8_scaled_mm_torch_cpu(qa[:4], b, sa[:4], sw, torch.bfloat16)  # warm-up
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        ops.fp8_scaled_mm_torch_cpu(qa, b, sa, sw, torch.bfloat16)
+        times.append(time.perf_counter() - t0)
+    sec = sorted(times)[len(times) // 2]
+    flops = 2.0 * m_sample * 12288 * 2048
+    return {
+        "value": round(flops / sec / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"gate_up W8A8 GEMM, {m_sample} of 4096 rows x N=12288 x K=2048 through "
+                  f"torch._scaled_mm on CPU (reference sglops.py:111-139), median of {runs}; "
+                  f"os.cpu_count()={os.cpu_count()}",
+        "seconds_per_sample": round(sec, 3),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--quick", action="store_true", help="headline GEMM only")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(the FP8 path is single-GPU; see the sharding note in DESIGN.md)", file=sys.stderr)
+        return 2
+    from flashrec_amd._lib import load
+
+    load()
+    dev = torch.device("cuda:0")
+    torch.backends.cuda.matmul.allow_tf32 = False
+
+    m, n, k = 4096, 12288, 2048
+    ms, tflops = _gemm_case(dev, m, n, k, args.steps, args.warmup, seed=1)
+    result = {
+        "metric": "FP8 GEMM TFLOPS + quant/KV-write GB/s at 512-4096 beam rows; % of roofline",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "e4m3 (fp32 accumulate, bf16 out)",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights; operands rotated over >512 MB)",
+        "config": {"workload": "config1 gate_up W8A8 GEMM", "M": m, "N": n, "K": k,
+                   "a": "e4m3 per-token scale", "b": "e4m3 per-channel scale, column-major"},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP8_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP8_TFLOPS, 4),
+                     "traffic": None},
+    }
+    extra = {}
+    if not args.quick:
+        steps, warm = max(20, args.steps), args.warmup
+        ms1, tf1 = _gemm_case(dev, 512, 12288, 2048, steps, warm, seed=11)
+        extra["config1_gemm_M512"] = {"ms": round(ms1, 5), "TFLOP/s": round(tf1, 2),
+                                      "frac": round(tf1 / PEAK_FP8_TFLOPS, 4)}
+        ms2, tf2 = _gemm_case(dev, 4096, 2048, 6144, steps, warm, seed=2)
+        extra["config2_down_gemm"] = {"ms": round(ms2, 5), "TFLOP/s": round(tf2, 2),
+                                      "frac": round(tf2 / PEAK_FP8_TFLOPS, 4)}
+        for name, (mm, nn, kk) in {"config4_qkv_gemm": (4096, 4096, 2048),
+                                   "config4_o_gemm": (4096, 2048, 2048),
+                                   "config4_lm_head_gemm": (4096, 8192, 2048)}.items():
+            msx, tfx = _gemm_case(dev, mm, nn, kk, steps, warm, seed=5)
+            extra[name] = {"ms": round(msx, 5), "TFLOP/s": round(tfx, 2),
+                           "frac": round(tfx / PEAK_FP8_TFLOPS, 4)}
+        cases = {
+            "config0_rms_fp8_M512_cached": _rms_case(dev, 512, 2048, rotate=False),
+            "config0_rms_fp8_M4096": _rms_case(dev, 4096, 2048, rotate=True),
+            "rms_fp8_M65536": _rms_case(dev, 65536, 2048, rotate=True),
+            "config2_silu_fp8": _silu_case(dev, 4096, 6144, rotate=True),
+            "config3_qk_rope_kv": _rope_case(dev, 4096, 16, 8, 128, 65536, rotate=True),
+            "qk_rope_kv_T32768": _rope_case(dev, 32768, 16, 8, 128, 65536, rotate=True),
+        }
+        for name, (factory, nbytes) in cases.items():
+            msb, gbs = _bw_case(factory, dev, steps, warm, nbytes)
+            extra[name] = {"ms": round(msb, 5), "GB/s": round(gbs, 1),
+                           "frac": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes}
+            torch.cuda.empty_cache()
+        result["extra"] = extra
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,175 @@
+// Shared device helpers for the FlashRec FP8 path on MI355X (gfx950, CDNA4).
+//
+// Numeric conventions follow the torch CPU arithmetic of the reference's
+// fallback path (python/flashrec/kernel/sglops.py:33-151):
+//   * bf16 <-> fp32 conversions are exact widening / round-to-nearest-even;
+//   * float -> float8_e4m3fn follows torch's c10 conversion: round to nearest
+//     even, |x| > 464 (and NaN/inf) -> NaN code 0x7F | sign;
+//   * divisions and square roots are IEEE correctly rounded.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define FR_OK 0
+#define FR_EINVAL 1      // bad pointer / size / stride
+#define FR_EUNSUPPORTED 2  // shape the kernels do not handle (caller falls back)
+#define FR_ELAUNCH 3     // HIP launch error
+
+#define FR_DTYPE_BF16 0
+#define FR_DTYPE_FP16 1
+#define FR_DTYPE_FP32 2
+#define FR_DTYPE_E4M3 3
+
+namespace fr {
+
+constexpr float kFp8Max = 448.0f;
+constexpr float kAmaxFloor = 1e-12f;
+
+// ---------------------------------------------------------------- bf16 / fp16
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (gfx950 v_cvt_pk_bf16_f32; NaN stays NaN).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  bf2 v;
+  v[0] = static_cast<__bf16>(lo);
+  v[1] = static_cast<__bf16>(hi);
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ float round_bf16(float x) {
+  return bf16_to_f32(static_cast<uint16_t>(pack_bf16x2(x, 0.0f) & 0xFFFFu));
+}
+
+__device__ __forceinline__ float fp16_to_f32(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+__device__ __forceinline__ uint32_t pack_fp16x2(float lo, float hi) {
+  _Float16 a = static_cast<_Float16>(lo);
+  _Float16 b = static_cast<_Float16>(hi);
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
+}
+
+// Element loader: the activation dtype is a template parameter so the row
+// kernels read bf16, fp16 or fp32 without a runtime branch.
+template <int DT>
+struct Elem;
+template <>
+struct Elem<FR_DTYPE_BF16> {
+  using T = uint16_t;
+  static __device__ __forceinline__ float load(const T* p) { return bf16_to_f32(*p); }
+};
+template <>
+struct Elem<FR_DTYPE_FP16> {
+  using T = uint16_t;
+  static __device__ __forceinline__ float load(const T* p) { return fp16_to_f32(*p); }
+};
+template <>
+struct Elem<FR_DTYPE_FP32> {
+  using T = float;
+  static __device__ __forceinline__ float load(const T* p) { return *p; }
+};
+
+// ---------------------------------------------------------------- e4m3
+// Hardware pack of two fp32 values already inside [-448, 448] into e4m3
+// (v_cvt_pk_fp8_f32, OCP e4m3 on gfx950, round to nearest even).
+template <bool HI>
+__device__ __forceinline__ uint32_t cvt_pk_e4m3(float a, float b, uint32_t old) {
+  return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, static_cast<int>(old), HI));
+}
+
+__device__ __forceinline__ float sat448(float x) {
+  return __builtin_fminf(__builtin_fmaxf(x, -kFp8Max), kFp8Max);
+}
+
+// Torch semantics of `t.to(float8_e4m3fn)` for one value, returned as the
+// replacement byte (0x7F|sign) when the value is NaN or beyond 464, else
+// `ok=true` and the caller converts sat448(x) in hardware.
+__device__ __forceinline__ bool e4m3_in_range(float x) {
+  return __builtin_fabsf(x) <= 464.0f;  // false for NaN
+}
+
+__device__ __forceinline__ uint32_t e4m3_nan_byte(float x) {
+  return (__float_as_uint(x) >> 24 & 0x80u) | 0x7Fu;
+}
+
+// Four values -> four e4m3 bytes packed little-endian, torch `.to(e4m3)`
+// semantics (no prior clamp).
+__device__ __forceinline__ uint32_t e4m3x4_torch(float a, float b, float c, float d) {
+  uint32_t w = cvt_pk_e4m3<false>(sat448(a), sat448(b), 0u);
+  w = cvt_pk_e4m3<true>(sat448(c), sat448(d), w);
+  if (!(e4m3_in_range(a) && e4m3_in_range(b) && e4m3_in_range(c) && e4m3_in_range(d))) {
+    float v[4] = {a, b, c, d};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (!e4m3_in_range(v[i])) {
+        w = (w & ~(0xFFu << (8 * i))) | (e4m3_nan_byte(v[i]) << (8 * i));
+      }
+    }
+  }
+  return w;
+}
+
+// Four values that went through torch's `.clamp(-448, 448)` first: NaN
+// survives a torch clamp, so only NaN needs the replacement byte.
+__device__ __forceinline__ uint32_t e4m3x4_clamped(float a, float b, float c, float d) {
+  uint32_t w = cvt_pk_e4m3<false>(sat448(a), sat448(b), 0u);
+  w = cvt_pk_e4m3<true>(sat448(c), sat448(d), w);
+  if (__builtin_expect((a != a) | (b != b) | (c != c) | (d != d), 0)) {
+    float v[4] = {a, b, c, d};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (v[i] != v[i]) w = (w & ~(0xFFu << (8 * i))) | (e4m3_nan_byte(v[i]) << (8 * i));
+    }
+  }
+  return w;
+}
+
+__device__ __forceinline__ uint32_t e4m3_torch_byte(float x) {
+  return e4m3x4_torch(x, 0.f, 0.f, 0.f) & 0xFFu;
+}
+__device__ __forceinline__ uint32_t e4m3_clamped_byte(float x) {
+  return e4m3x4_clamped(x, 0.f, 0.f, 0.f) & 0xFFu;
+}
+
+// ---------------------------------------------------------------- division
+// Correctly rounded x / s for a divisor shared by a whole row, with r the
+// correctly rounded reciprocal 1/s.  One mul + two fma (Markstein's
+// correction step: with y faithful and r = RN(1/s), RN(y + r*(x - s*y)) is
+// RN(x/s) barring under/overflow).  The row kernels only call this when s is
+// finite and normal; otherwise they use the plain IEEE division.
+__device__ __forceinline__ float div_rn_shared(float x, float s, float r) {
+  float y = x * r;
+  float e = __builtin_fmaf(-y, s, x);
+  return __builtin_fmaf(e, r, y);
+}
+
+// ---------------------------------------------------------------- wave64 reductions
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+// Reduction over aligned groups of G lanes (G a power of two <= 64).
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = G / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// 16-byte vector type for coalesced loads/stores.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+}  // namespace fr

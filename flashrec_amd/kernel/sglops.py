@@ -1,0 +1,252 @@
+"""Operator wrappers with the signatures of ``flashrec.kernel.sglops``.
+
+Reference: python/flashrec/kernel/sglops.py.  Each function keeps the
+reference's name, arguments, return convention and in-place behaviour, but
+runs a hand-written HIP kernel through the C ABI.  Unlike the reference there
+is no CPU branch: CPU tensors raise (a silent torch fallback would hide a
+missing or broken native library).
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from flashrec_amd._lib import DTYPE_CODE, call, ptr, require_device, stream_of
+
+_FP8_MAX = 448.0
+
+
+def _bf16_vec(weight: torch.Tensor, device: torch.device) -> torch.Tensor:
+    return weight.reshape(-1).to(device=device, dtype=torch.bfloat16).contiguous()
+
+
+def _rows(x: torch.Tensor, width: int) -> torch.Tensor:
+    """[..., width] -> [rows, width] with unit inner stride (copy only if needed)."""
+    x2 = x.reshape(-1, width)
+    if x2.stride(-1) != 1 or (x2.shape[0] > 1 and x2.stride(0) < width):
+        x2 = x2.contiguous()
+    return x2
+
+
+@torch.compiler.disable
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """``(x * rsqrt(mean(x^2) + eps)) * weight`` per row (sglops.py:33-45)."""
+    require_device(x)
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"rmsnorm takes bf16 activations, got {x.dtype}")
+    orig = x.shape
+    hidden = int(weight.numel())
+    x2 = _rows(x, hidden)
+    w = _bf16_vec(weight, x.device)
+    out = torch.empty(x2.shape, dtype=x.dtype, device=x.device)
+    call("fr_rmsnorm", x2.data_ptr(), x2.stride(0), None, 0, w.data_ptr(), out.data_ptr(),
+         out.stride(0), x2.shape[0], hidden, float(eps), stream_of(x))
+    return out.view(orig)
+
+
+@torch.compiler.disable
+def fused_add_rmsnorm(
+    x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """``residual += x`` then RMSNorm(residual). Mutates both (sglops.py:48-61)."""
+    require_device(x, residual)
+    if x.dtype != torch.bfloat16 or residual.dtype != torch.bfloat16:
+        raise TypeError("fused_add_rmsnorm takes bf16 x and residual")
+    hidden = int(weight.numel())
+    x2 = x.reshape(-1, hidden).contiguous()
+    r2 = residual.reshape(-1, hidden).contiguous()
+    w = _bf16_vec(weight, x.device)
+    call("fr_rmsnorm", x2.data_ptr(), x2.stride(0), r2.data_ptr(), r2.stride(0), w.data_ptr(),
+         x2.data_ptr(), x2.stride(0), x2.shape[0], hidden, float(eps), stream_of(x))
+    return x2.reshape(x.shape), r2.reshape(residual.shape)
+
+
+@torch.compiler.disable
+def apply_rope_inplace(
+    positions: torch.Tensor,
+    query: torch.Tensor,
+    key: torch.Tensor,
+    head_size: int,
+    cos_sin_cache: torch.Tensor,
+) -> bool:
+    """NeoX RoPE of ``query`` [T, Hq*D] and ``key`` [T, Hk*D] in place (sglops.py:64-81).
+
+    Returns True when the kernel ran; False for layouts it does not take
+    (the reference returns False when its backend is absent).
+    """
+    require_device(query, key)
+    d = int(head_size)
+    t = int(positions.numel())
+    if query.dtype != torch.bfloat16 or key.dtype != torch.bfloat16:
+        return False
+    if d <= 0 or d > 128 or d % 2 or int(cos_sin_cache.shape[-1]) != d:
+        return False
+    q3 = query.view(t, -1, d)
+    k3 = key.view(t, -1, d)
+    if q3.stride(-1) != 1 or k3.stride(-1) != 1:
+        return False
+    pos = positions.view(-1).to(dtype=torch.int64).contiguous()
+    cs = cos_sin_cache.to(device=query.device, dtype=torch.float32).contiguous()
+    call("fr_rope_inplace", q3.data_ptr(), q3.stride(0), q3.stride(1), k3.data_ptr(),
+         k3.stride(0), k3.stride(1), pos.data_ptr(), cs.data_ptr(), cs.shape[0], t,
+         q3.shape[1], k3.shape[1], d, stream_of(query))
+    return True
+
+
+@torch.compiler.disable
+def per_token_quant_fp8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row absmax e4m3 quant: ``(q [M,K] e4m3, scale [M,1] fp32)`` (sglops.py:84-96)."""
+    require_device(x)
+    if x.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise TypeError(f"per_token_quant_fp8 takes bf16/fp16/fp32, got {x.dtype}")
+    x2 = _rows(x, x.shape[-1])
+    q = torch.empty(x2.shape, dtype=torch.float8_e4m3fn, device=x2.device)
+    s = torch.empty((x2.shape[0], 1), dtype=torch.float32, device=x2.device)
+    call("fr_per_token_quant_fp8", x2.data_ptr(), DTYPE_CODE[x2.dtype], x2.shape[0],
+         x2.shape[1], x2.stride(0), q.data_ptr(), s.data_ptr(), stream_of(x2))
+    return q, s
+
+
+@torch.compiler.disable
+def fp8_scaled_mm(
+    a_fp8: torch.Tensor,
+    b_fp8: torch.Tensor,
+    scale_a: torch.Tensor,
+    scale_b: torch.Tensor,
+    out_dtype: torch.dtype,
+    bias: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """a: [M,K] fp8, b: [K,N] fp8 (column-major), scale_a: [M,1], scale_b: [N] (sglops.py:99-140)."""
+    require_device(a_fp8, b_fp8)
+    if a_fp8.dtype != torch.float8_e4m3fn or b_fp8.dtype != torch.float8_e4m3fn:
+        raise TypeError("fp8_scaled_mm takes float8_e4m3fn operands")
+    if out_dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise TypeError(f"unsupported out_dtype {out_dtype}")
+    if a_fp8.dim() != 2 or b_fp8.dim() != 2 or a_fp8.shape[1] != b_fp8.shape[0]:
+        raise ValueError(f"shape mismatch: a {tuple(a_fp8.shape)} b {tuple(b_fp8.shape)}")
+    m, k = int(a_fp8.shape[0]), int(a_fp8.shape[1])
+    n = int(b_fp8.shape[1])
+    a = a_fp8 if a_fp8.stride(1) == 1 and (m <= 1 or a_fp8.stride(0) >= k) else a_fp8.contiguous()
+    b = b_fp8
+    if not (b.stride(0) == 1 and (n <= 1 or b.stride(1) >= k)):
+        b = b.t().contiguous().t()  # column-major copy
+    sa = scale_a.reshape(-1).to(device=a.device, dtype=torch.float32).contiguous()
+    sb = scale_b.reshape(-1).to(device=a.device, dtype=torch.float32).contiguous()
+    if sa.numel() not in (1, m) or sb.numel() not in (1, n):
+        raise ValueError("scale_a must have 1 or M values and scale_b 1 or N values")
+    bias_t = None
+    if bias is not None:
+        bias_t = bias.reshape(-1).to(device=a.device, dtype=out_dtype).contiguous()
+    out = torch.empty((m, n), dtype=out_dtype, device=a.device)
+    lda = a.stride(0) if m > 1 else k
+    ldb = b.stride(1) if n > 1 else k
+    call("fr_fp8_scaled_mm", a.data_ptr(), lda, b.data_ptr(), ldb, sa.data_ptr(), sa.numel(),
+         sb.data_ptr(), sb.numel(), ptr(bias_t), out.data_ptr(), out.stride(0), m, n, k,
+         DTYPE_CODE[out_dtype], stream_of(a))
+    return out
+
+
+@torch.compiler.disable
+def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
+    """SwiGLU: ``silu(x[..., :d]) * x[..., d:]`` with ``d = last_dim // 2`` (sglops.py:143-151)."""
+    require_device(x)
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"silu_and_mul takes bf16, got {x.dtype}")
+    last = int(x.shape[-1])
+    if last % 2:
+        raise ValueError("silu_and_mul needs an even last dimension")
+    d = last // 2
+    x2 = _rows(x, last)
+    out = torch.empty((x2.shape[0], d), dtype=x.dtype, device=x.device)
+    call("fr_silu_and_mul", x2.data_ptr(), x2.stride(0), out.data_ptr(), out.stride(0),
+         x2.shape[0], d, stream_of(x))
+    return out.view(*x.shape[:-1], d)
+
+
+@torch.compiler.disable
+def apply_rope_and_store_kv(
+    positions: torch.Tensor,
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    loc: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    head_size: int,
+    cos_sin_cache: torch.Tensor,
+) -> bool:
+    """Fused RoPE + KV store for matching dtypes (sglops.py:154-204).
+
+    The reference returns False whenever the cache dtype differs from the
+    activations (every fp8-KV configuration), and the FP8 path always has an
+    fp8 cache, so this returns False for that case and the caller goes
+    through ``fused_qk_norm_rope_store_fp8`` / ``TokenToKVPool.store``.
+    """
+    require_device(query, key, value)
+    if key.dtype != k_cache.dtype or value.dtype != v_cache.dtype:
+        return False
+    return False
+
+
+@torch.compiler.disable
+def store_kv_cache(
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    loc: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+) -> None:
+    """``k_cache[loc] = k; v_cache[loc] = v`` on rows of width row_dim (sglops.py:207-222).
+
+    Caches are e4m3 ``[slots, row_dim]``; k/v are e4m3 (copied) or bf16
+    (converted with torch's ``.to(float8_e4m3fn)`` rounding).  Slots outside
+    ``[0, slots)`` are skipped instead of raising an IndexError.
+    """
+    require_device(k_cache, v_cache, k, v)
+    if k_cache.dtype != torch.float8_e4m3fn or v_cache.dtype != torch.float8_e4m3fn:
+        raise TypeError("store_kv_cache writes float8_e4m3fn caches")
+    slots = int(k_cache.shape[0])
+    row_dim = int(k_cache[0].numel()) if slots else int(k.shape[-1])
+    kc = k_cache.view(slots, row_dim)
+    vc = v_cache.view(slots, row_dim)
+    loc64 = loc.view(-1).to(dtype=torch.int64).contiguous()
+    n = int(loc64.numel())
+    k2 = k.reshape(n, row_dim)
+    v2 = v.reshape(n, row_dim)
+    if k2.dtype != v2.dtype or k2.dtype not in (torch.bfloat16, torch.float8_e4m3fn):
+        raise TypeError("k/v must both be bf16 or both float8_e4m3fn")
+    if k2.stride(-1) != 1:
+        k2 = k2.contiguous()
+    if v2.stride(-1) != 1:
+        v2 = v2.contiguous()
+    call("fr_store_kv_fp8", k2.data_ptr(), k2.stride(0), v2.data_ptr(), v2.stride(0),
+         DTYPE_CODE[k2.dtype], loc64.data_ptr(), kc.data_ptr(), kc.stride(0), vc.data_ptr(),
+         vc.stride(0), slots, n, row_dim, stream_of(k_cache))
+
+
+@torch.compiler.disable
+def log_softmax_f32(logits: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Row-wise ``log_softmax`` of fp32 logits (the tail of logits.py:118-120)."""
+    require_device(logits)
+    if logits.dtype != torch.float32 or logits.dim() != 2 or logits.stride(1) != 1:
+        raise TypeError("log_softmax_f32 takes 2-D fp32 logits with unit inner stride")
+    if out is None:
+        out = torch.empty_like(logits)
+    call("fr_log_softmax_f32", logits.data_ptr(), logits.stride(0), out.data_ptr(),
+         out.stride(0), logits.shape[0], logits.shape[1], stream_of(logits))
+    return out
+
+
+__all__ = [
+    "rmsnorm",
+    "fused_add_rmsnorm",
+    "apply_rope_inplace",
+    "per_token_quant_fp8",
+    "fp8_scaled_mm",
+    "silu_and_mul",
+    "apply_rope_and_store_kv",
+    "store_kv_cache",
+    "log_softmax_f32",
+]

@@ -1,0 +1,132 @@
+/*
+ * flashrec_amd: C ABI of the MI355X (gfx950) FP8 quantized compute path.
+ *
+ * Every entry point takes raw device pointers, element strides and a
+ * hipStream_t (passed as void*), launches on that stream, never allocates,
+ * never synchronises and never reads device memory from the host, so all of
+ * them are safe to record into a HIP graph.  Return value: FR_OK (0) or one
+ * of the FR_E* codes below.  Dtype codes: 0 bf16, 1 fp16, 2 fp32, 3 e4m3fn.
+ *
+ * Each declaration cites the reference interface it replaces
+ * (paths relative to the sohu-mptc/FlashRec tree).
+ */
+#ifndef FLASHREC_AMD_H
+#define FLASHREC_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FR_OK 0
+#define FR_EINVAL 1        /* null pointer, negative size, bad stride/scale size */
+#define FR_EUNSUPPORTED 2  /* valid request the kernels do not handle; caller falls back */
+#define FR_ELAUNCH 3       /* HIP reported a launch error */
+
+#define FR_DTYPE_BF16 0
+#define FR_DTYPE_FP16 1
+#define FR_DTYPE_FP32 2
+#define FR_DTYPE_E4M3 3
+
+/* ABI revision of this header (1). */
+int fr_abi_version(void);
+
+/* Per-token (per-row) e4m3 quantisation.
+ * x: [M, K] of x_dtype (bf16/fp16/fp32) with row stride ldx (elements);
+ * q: [M, K] e4m3 contiguous; s: [M] fp32, s = max(amax|x|, 1e-12) / 448,
+ * q = e4m3(clamp(x / s, -448, 448)).
+ * Replaces python/flashrec/kernel/sglops.py:84-96 (per_token_quant_fp8). */
+int fr_per_token_quant_fp8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                           void* q, float* s, void* stream);
+
+/* Per-output-channel weight quantisation: w [N, K] -> q [N, K] e4m3, s [N].
+ * Same arithmetic as fr_per_token_quant_fp8 along the rows of W.
+ * Replaces python/flashrec/layers/linear.py:26-32 (quantize_weight_fp8). */
+int fr_quantize_weight_fp8(const void* w, int w_dtype, int64_t N, int64_t K, int64_t ldw,
+                           void* q, float* s, void* stream);
+
+/* RMSNorm (optionally after `residual += x`, residual updated in place as
+ * bf16) fused with per-token e4m3 quantisation.  x, residual, w: bf16.
+ * residual may be NULL.  q: [M, H] e4m3 contiguous, s: [M] fp32.
+ * Replaces python/flashrec/kernel/rms_fp8.py:120-145
+ * (rmsnorm_per_token_quant_fp8, fused_add_rmsnorm_per_token_quant_fp8). */
+int fr_rms_quant_fp8(const void* x, int64_t ldx, void* residual, int64_t ldr, const void* w,
+                     int64_t M, int64_t H, float eps, void* q, float* s, void* stream);
+
+/* RMSNorm with bf16 output (out may alias x); with residual != NULL it is
+ * fused_add_rmsnorm: residual = bf16(residual + x), out = rmsnorm(residual).
+ * Replaces python/flashrec/kernel/sglops.py:33-45 (rmsnorm) and :48-61
+ * (fused_add_rmsnorm). */
+int fr_rmsnorm(const void* x, int64_t ldx, void* residual, int64_t ldr, const void* w,
+               void* out, int64_t ldo, int64_t M, int64_t H, float eps, void* stream);
+
+/* SiLU-and-mul over [M, 2d] bf16 rows (gate half first) fused with per-token
+ * e4m3 quantisation: q [M, d] e4m3 contiguous, s [M] fp32.
+ * Replaces python/flashrec/kernel/silu_fp8.py:85-119
+ * (silu_and_mul_per_token_quant_fp8). */
+int fr_silu_quant_fp8(const void* x, int64_t ldx, int64_t M, int64_t d, void* q, float* s,
+                      void* stream);
+
+/* SiLU-and-mul with bf16 output [M, d] (row stride ldo).
+ * Replaces python/flashrec/kernel/sglops.py:143-151 (silu_and_mul). */
+int fr_silu_and_mul(const void* x, int64_t ldx, void* out, int64_t ldo, int64_t M, int64_t d,
+                    void* stream);
+
+/* W8A8 GEMM: out[m, n] = (sum_k a[m, k] b[k, n]) * scale_a[m] * scale_b[n]
+ * (+ bias[n]).  a: [M, K] e4m3 row-major (row stride lda bytes);
+ * b: [K, N] e4m3 column-major (column n at b + n * ldb); scale_a numel 1 or
+ * M, scale_b numel 1 or N (fp32); bias: out_dtype [N] or NULL; out: [M, N]
+ * of out_dtype (bf16, fp16 or fp32) with row stride ldo (elements).
+ * Replaces python/flashrec/kernel/sglops.py:99-140 (fp8_scaled_mm). */
+int fr_fp8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
+                     const float* scale_a, int64_t scale_a_numel, const float* scale_b,
+                     int64_t scale_b_numel, const void* bias, void* out, int64_t ldo, int64_t M,
+                     int64_t N, int64_t K, int out_dtype, void* stream);
+
+/* Per-head RMSNorm of q and k (weights q_weight, k_weight: bf16 [D]),
+ * NeoX rotate-half RoPE from cos_sin_cache ([cache_rows, D] fp32: cos for
+ * i < D/2, sin after), q rotated in place (bf16), rotated k and raw v
+ * written unscaled as e4m3 into k_cache[loc[t], h, :] / v_cache[loc[t], h, :].
+ * q: [T, Hq, D], k/v: [T, Hk, D] bf16 with (token, head) strides in
+ * elements; positions/loc: int64 [T]; cache strides in bytes (e4m3).
+ * Slots outside [0, num_slots) and positions outside [0, cache_rows) are
+ * skipped.  D must be even and <= 128 (else FR_EUNSUPPORTED).
+ * Replaces python/flashrec/kernel/qk_rope_kv.py:164-250
+ * (fused_qk_norm_rope_store_fp8). */
+int fr_qk_norm_rope_store_fp8(void* q, int64_t sqt, int64_t sqh, const void* k, int64_t skt,
+                              int64_t skh, const void* v, int64_t svt, int64_t svh,
+                              const int64_t* positions, const int64_t* loc, const void* q_weight,
+                              const void* k_weight, float eps, const float* cos_sin_cache,
+                              int64_t cache_rows, void* k_cache, int64_t sckp, int64_t sckh,
+                              void* v_cache, int64_t scvp, int64_t scvh, int64_t num_slots,
+                              int64_t T, int64_t Hq, int64_t Hk, int64_t D, void* stream);
+
+/* NeoX rotate-half RoPE of q [T, Hq, D] and k [T, Hk, D] (bf16) in place,
+ * no normalisation, no KV store; same cos_sin_cache layout and rounding as
+ * fr_qk_norm_rope_store_fp8.
+ * Replaces python/flashrec/kernel/sglops.py:64-81 (apply_rope_inplace). */
+int fr_rope_inplace(void* q, int64_t sqt, int64_t sqh, void* k, int64_t skt, int64_t skh,
+                    const int64_t* positions, const float* cos_sin_cache, int64_t cache_rows,
+                    int64_t T, int64_t Hq, int64_t Hk, int64_t D, void* stream);
+
+/* KV store: k/v rows [T, row_dim] (bf16 -> e4m3 with torch conversion
+ * semantics, or e4m3 copied as bytes) scattered to k_cache/v_cache rows
+ * loc[t] (row strides sck/scv bytes).  Slots outside [0, num_slots) are
+ * skipped.
+ * Replaces python/flashrec/kvcache/pool.py:121-139 (TokenToKVPool.store)
+ * and python/flashrec/kernel/sglops.py:207-222 (store_kv_cache). */
+int fr_store_kv_fp8(const void* k, int64_t skt, const void* v, int64_t svt, int src_dtype,
+                    const int64_t* loc, void* k_cache, int64_t sck, void* v_cache, int64_t scv,
+                    int64_t num_slots, int64_t T, int64_t row_dim, void* stream);
+
+/* Row-wise log_softmax of fp32 logits [M, N] (out may alias x).
+ * Replaces the log_softmax of python/flashrec/logits.py:118-120, :136-137. */
+int fr_log_softmax_f32(const float* x, int64_t ldx, float* out, int64_t ldo, int64_t M,
+                       int64_t N, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASHREC_AMD_H */

@@ -1,0 +1,62 @@
+"""Comparison helpers shared by the parity tests."""
+
+from __future__ import annotations
+
+import torch
+
+
+def codes(t: torch.Tensor) -> torch.Tensor:
+    """e4m3 tensor -> int16 codes on the CPU."""
+    return t.detach().cpu().contiguous().view(torch.uint8).to(torch.int16)
+
+
+def code_flip_stats(q_got: torch.Tensor, q_ref: torch.Tensor):
+    """(fraction of differing codes, max distance between differing codes of the same sign)."""
+    a, b = codes(q_got), codes(q_ref)
+    diff = a != b
+    frac = diff.float().mean().item()
+    if not diff.any():
+        return 0.0, 0
+    same_sign = ((a ^ b) & 0x80) == 0
+    dist = torch.where(diff & same_sign, (a - b).abs(), torch.full_like(a, 255))
+    # zero may be encoded with either sign when the value rounds to 0
+    zero_pair = diff & ((a & 0x7F) == 0) & ((b & 0x7F) <= 1) | diff & ((b & 0x7F) == 0) & ((a & 0x7F) <= 1)
+    dist = torch.where(zero_pair, torch.ones_like(dist), dist)
+    return frac, int(dist[diff].max().item())
+
+
+def assert_fp8_parity(q_got, s_got, q_ref, s_ref, max_flip_frac=1e-3):
+    """The bar for quantised outputs whose pre-quant value is summed or passed
+    through exp in a different order than torch's CPU: codes and scales
+    bit-exact except <= 1-ULP flips on < 0.1% of elements."""
+    s_got = s_got.detach().cpu().float().reshape(-1)
+    s_ref = s_ref.detach().cpu().float().reshape(-1)
+    sdiff = s_got != s_ref
+    if sdiff.any():
+        rel = ((s_got - s_ref).abs() / s_ref.abs().clamp(min=1e-30))[sdiff]
+        # amax is a bf16 value: a flip moves it by one bf16 ULP (2^-8 relative)
+        assert rel.max().item() <= 2.0 ** -7, f"scale off by {rel.max().item()}"
+        assert sdiff.float().mean().item() < max_flip_frac * 10, "too many rows changed scale"
+    frac, dist = code_flip_stats(q_got, q_ref)
+    assert dist <= 1, f"codes differ by {dist} ULP"
+    assert frac < max_flip_frac, f"{frac:.2e} of codes flipped"
+
+
+def assert_bf16_parity(got, ref, max_flip_frac=1e-3):
+    """bf16 outputs: bit-exact except 1-ULP flips on < 0.1% of elements."""
+    a = got.detach().cpu().contiguous().view(torch.int16).to(torch.int32)
+    b = ref.detach().cpu().contiguous().view(torch.int16).to(torch.int32)
+    diff = a != b
+    if not diff.any():
+        return
+    dist = (a - b).abs()[diff].max().item()
+    frac = diff.float().mean().item()
+    assert dist <= 1, f"bf16 values differ by {dist} ULP"
+    assert frac < max_flip_frac, f"{frac:.2e} of bf16 values flipped"
+
+
+def max_abs_rel(got: torch.Tensor, ref: torch.Tensor) -> float:
+    """max |got - ref| / max |ref|  (the GEMM acceptance metric)."""
+    got = got.detach().cpu().float()
+    ref = ref.detach().cpu().float()
+    return ((got - ref).abs().max() / ref.abs().max().clamp(min=1e-30)).item()

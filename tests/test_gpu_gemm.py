@@ -1,0 +1,127 @@
+"""Parity of the W8A8 fp8 GEMM with the fp32 dequantised-matmul oracle.
+
+Acceptance: bf16 outputs within 1e-2 of the oracle, relative to the
+output's max |value| (max-abs normalised).  Integer-valued operands with
+unit scales make the product exact, which pins the accumulation itself.
+"""
+
+import pytest
+import torch
+
+from helpers import max_abs_rel
+from oracle import inputs, ops
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+def _operands(m, n, k, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    w = (0.02 * torch.randn(n, k, generator=g)).to(torch.bfloat16)
+    qa, sa = ops.per_token_quant_fp8(x)
+    qw, sw = ops.quantize_weight_fp8(w)
+    return qa, sa, qw, sw
+
+
+def _run(dev, qa, sa, qw, sw, out_dtype=torch.bfloat16, bias=None):
+    from flashrec_amd.kernel.sglops import fp8_scaled_mm
+
+    b = qw.to(dev).t()  # [K, N] column-major view, as Linear keeps it
+    return fp8_scaled_mm(qa.to(dev), b, sa.to(dev), sw.to(dev), out_dtype,
+                         None if bias is None else bias.to(dev))
+
+
+@pytest.mark.parametrize("m,n,k", [(4, 128, 64), (1, 256, 2048), (33, 100, 256), (300, 520, 384),
+                                   (128, 128, 128), (512, 4096, 2048), (256, 2048, 6144),
+                                   (64, 8192, 2048), (17, 48, 48)])
+def test_gemm_vs_dequant_oracle(dev, m, n, k):
+    qa, sa, qw, sw = _operands(m, n, k, seed=m + n + k)
+    out = _run(dev, qa, sa, qw, sw)
+    assert out.dtype == torch.bfloat16 and out.shape == (m, n)
+    ref = ops.fp8_scaled_mm(qa, qw.t(), sa, sw)
+    assert max_abs_rel(out, ref) < TOL
+
+
+def test_gemm_integer_exact(dev):
+    """Small-integer e4m3 operands, unit scales, fp32 out: the product is exact."""
+    g = torch.Generator().manual_seed(0)
+    m, n, k = 256, 512, 1024
+    a = torch.randint(-4, 5, (m, k), generator=g).float()
+    w = torch.randint(-4, 5, (n, k), generator=g).float()
+    qa, qw = a.to(torch.float8_e4m3fn), w.to(torch.float8_e4m3fn)
+    one_m = torch.ones(m, 1)
+    one_n = torch.ones(n)
+    out = _run(dev, qa, one_m, qw, one_n, out_dtype=torch.float32)
+    ref = (a.to(torch.int64) @ w.to(torch.int64).t()).float()
+    assert torch.equal(out.cpu(), ref)
+
+
+def test_gemm_onehot_columns(dev):
+    """One-hot K rows pick single products: catches transposed / shifted operands."""
+    m, n, k = 64, 256, 256
+    a = torch.zeros(m, k)
+    a[torch.arange(m), (torch.arange(m) * 7) % k] = 1.0
+    w = torch.arange(n * k, dtype=torch.float32).reshape(n, k) % 13 - 6
+    qa, qw = a.to(torch.float8_e4m3fn), w.to(torch.float8_e4m3fn)
+    sa = torch.full((m, 1), 0.5)
+    sw = torch.linspace(1, 2, n)
+    out = _run(dev, qa, sa, qw, sw, out_dtype=torch.float32)
+    ref = ops.fp8_scaled_mm(qa, qw.t(), sa, sw)
+    assert torch.equal(out.cpu(), ref)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.float32])
+def test_gemm_out_dtypes_and_bias(dev, out_dtype):
+    qa, sa, qw, sw = _operands(96, 640, 512, seed=4)
+    bias = torch.randn(640).to(out_dtype)
+    out = _run(dev, qa, sa, qw, sw, out_dtype=out_dtype, bias=bias)
+    assert out.dtype == out_dtype
+    ref = ops.fp8_scaled_mm(qa, qw.t(), sa, sw, bias=bias.float())
+    assert max_abs_rel(out, ref) < TOL
+
+
+def test_gemm_per_tensor_scales(dev):
+    qa, _, qw, _ = _operands(40, 200, 256, seed=6)
+    sa = torch.tensor([0.25])
+    sw = torch.tensor([3.0])
+    out = _run(dev, qa, sa, qw, sw)
+    ref = ops.fp8_scaled_mm(qa, qw.t(), sa, sw)
+    assert max_abs_rel(out, ref) < TOL
+
+
+def test_gemm_scalar_path_odd_k(dev):
+    """K not a multiple of 16 takes the scalar kernel; same result bar."""
+    qa, sa, qw, sw = _operands(9, 70, 40, seed=8)
+    out = _run(dev, qa, sa, qw, sw, out_dtype=torch.float32)
+    ref = ops.fp8_scaled_mm(qa, qw.t(), sa, sw)
+    assert max_abs_rel(out, ref) < 1e-5
+
+
+def test_gemm_row_major_b_is_copied(dev):
+    from flashrec_amd.kernel.sglops import fp8_scaled_mm
+
+    qa, sa, qw, sw = _operands(16, 64, 128, seed=2)
+    b_rowmajor = qw.t().contiguous().to(dev)  # [K, N] row-major
+    out = fp8_scaled_mm(qa.to(dev), b_rowmajor, sa.to(dev), sw.to(dev), torch.bfloat16)
+    ref = ops.fp8_scaled_mm(qa, qw.t(), sa, sw)
+    assert max_abs_rel(out, ref) < TOL
+
+
+def test_gemm_config1_full_size_rows(dev):
+    """Config 1 at M=4096 (gate_up, K=2048, N=12288): every row of a seeded
+    sample of 96 rows against the oracle, plus the agreement of the full
+    output with the reference's literal torch._scaled_mm CPU branch on the
+    same rows."""
+    x, gamma, eps = inputs.config0(m=4096)
+    qa, sa = ops.rmsnorm_per_token_quant_fp8(x, gamma, eps)
+    qw, sw = ops.quantize_weight_fp8(inputs.config1_weight())
+    out = _run(dev, qa, sa, qw, sw)
+    rows = torch.randperm(4096, generator=torch.Generator().manual_seed(1))[:96]
+    ref = ops.fp8_scaled_mm(qa[rows], qw.t(), sa[rows], sw)
+    got = out.cpu()[rows]
+    assert max_abs_rel(got, ref) < TOL
+    lit = ops.fp8_scaled_mm_torch_cpu(qa[rows], qw.t(), sa[rows], sw, torch.bfloat16)
+    assert max_abs_rel(got, lit.float()) < TOL
+    assert torch.isfinite(out).all()

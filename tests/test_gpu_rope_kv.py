@@ -1,0 +1,170 @@
+"""Parity of the fused QK-norm + RoPE + fp8 KV write and of the KV store."""
+
+import pytest
+import torch
+
+from helpers import assert_bf16_parity, code_flip_stats, codes
+from oracle import inputs, ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(dev, q, k, v, pos, loc, qw, kw, eps, cache, slots, hk, d):
+    from flashrec_amd.kernel.qk_rope_kv import fused_qk_norm_rope_store_fp8
+
+    kc_ref = torch.zeros(slots, hk, d, dtype=torch.float8_e4m3fn)
+    vc_ref = torch.zeros_like(kc_ref)
+    q_ref = ops.qk_norm_rope_store_fp8(q, k, v, pos, loc, qw, kw, eps, cache, kc_ref, vc_ref)
+
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    kc = torch.zeros(slots, hk, d, dtype=torch.float8_e4m3fn, device=dev)
+    vc = torch.zeros_like(kc)
+    ok = fused_qk_norm_rope_store_fp8(qd, kd, vd, pos.to(dev), loc.to(dev), qw.to(dev), kw.to(dev),
+                                      eps, cache.to(dev), kc, vc)
+    assert ok
+    torch.cuda.synchronize()
+    assert_bf16_parity(qd, q_ref)
+    # V: pure conversion + scatter, bit-exact including untouched slots
+    assert torch.equal(codes(vc), codes(vc_ref))
+    frac, dist = code_flip_stats(kc, kc_ref)
+    assert dist <= 1 and frac < 1e-3
+    # k and v inputs are not modified
+    assert torch.equal(kd.cpu().view(torch.int16), k.view(torch.int16))
+    return qd, kc, vc
+
+
+def test_reference_case(dev):
+    """The shapes of the reference's tests/test_qk_rope_kv.py:10-63."""
+    torch.manual_seed(4)
+    t, hq, hk, d = 7, 16, 8, 128
+    cache = ops.cos_sin_cache(d, 2048, 1_000_000)
+    q = torch.randn(t, hq, d, dtype=torch.bfloat16)
+    k = torch.randn(t, hk, d, dtype=torch.bfloat16)
+    v = torch.randn(t, hk, d, dtype=torch.bfloat16)
+    pos = torch.arange(t, dtype=torch.int64) + 3
+    loc = torch.arange(1, t + 1, dtype=torch.int64)
+    ones = torch.ones(d, dtype=torch.bfloat16)
+    _check(dev, q, k, v, pos, loc, ones, ones, 1e-6, cache, t + 4, hk, d)
+
+
+def test_config3_full(dev):
+    q, k, v, pos, loc = inputs.config3()
+    cache = ops.cos_sin_cache(128, 4096, 1e6)
+    g = torch.Generator().manual_seed(13)
+    qw = (1 + 0.1 * torch.randn(128, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(128, generator=g)).to(torch.bfloat16)
+    _, kc, vc = _check(dev, q, k, v, pos, loc, qw, kw, 1e-6, cache, 65536, 8, 128)
+    # slot layout: written slots are exactly loc, everything else untouched (zero)
+    written = torch.zeros(65536, dtype=torch.bool)
+    written[loc] = True
+    vbytes = codes(vc).reshape(65536, -1)
+    assert (vbytes[~written] == 0).all()
+    assert (vbytes[written] != 0).any(dim=1).all()
+
+
+def test_strided_views_of_fused_qkv(dev):
+    """q/k/v as views into one [T, Hq+2Hk, D] buffer (how Qwen3Attention calls it)."""
+    t, hq, hk, d = 33, 16, 8, 128
+    g = torch.Generator().manual_seed(21)
+    qkv = torch.randn(t, hq + 2 * hk, d, generator=g).to(torch.bfloat16)
+    cache = ops.cos_sin_cache(d, 512, 1e6)
+    pos = torch.randint(0, 512, (t,), generator=g)
+    loc = torch.randperm(200, generator=g)[:t] + 1
+    w = torch.ones(d, dtype=torch.bfloat16)
+    q, k, v = qkv[:, :hq], qkv[:, hq:hq + hk], qkv[:, hq + hk:]
+    kc_ref = torch.zeros(201, hk, d, dtype=torch.float8_e4m3fn)
+    vc_ref = torch.zeros_like(kc_ref)
+    q_ref = ops.qk_norm_rope_store_fp8(q, k, v, pos, loc, w, w, 1e-6, cache, kc_ref, vc_ref)
+
+    from flashrec_amd.kernel.qk_rope_kv import fused_qk_norm_rope_store_fp8
+
+    qkv_d = qkv.to(dev)
+    kc = torch.zeros(201, hk, d, dtype=torch.float8_e4m3fn, device=dev)
+    vc = torch.zeros_like(kc)
+    assert fused_qk_norm_rope_store_fp8(qkv_d[:, :hq], qkv_d[:, hq:hq + hk], qkv_d[:, hq + hk:],
+                                        pos.to(dev), loc.to(dev), w.to(dev), w.to(dev), 1e-6,
+                                        cache.to(dev), kc, vc)
+    assert_bf16_parity(qkv_d[:, :hq], q_ref)
+    assert torch.equal(codes(vc), codes(vc_ref))
+    frac, dist = code_flip_stats(kc, kc_ref)
+    assert dist <= 1 and frac < 1e-3
+
+
+@pytest.mark.parametrize("hq,hk,d", [(6, 2, 64), (4, 4, 128), (3, 1, 100)])
+def test_generic_head_shapes(dev, hq, hk, d):
+    t = 9
+    g = torch.Generator().manual_seed(hq * 100 + d)
+    q = torch.randn(t, hq, d, generator=g).to(torch.bfloat16)
+    k = torch.randn(t, hk, d, generator=g).to(torch.bfloat16)
+    v = torch.randn(t, hk, d, generator=g).to(torch.bfloat16)
+    cache = ops.cos_sin_cache(d, 64, 1e4)
+    pos = torch.randint(0, 64, (t,), generator=g)
+    loc = torch.randperm(30, generator=g)[:t] + 1
+    w = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    _check(dev, q, k, v, pos, loc, w, w, 1e-6, cache, 31, hk, d)
+
+
+def test_unsupported_head_dim_returns_false(dev):
+    from flashrec_amd.kernel.qk_rope_kv import fused_qk_norm_rope_store_fp8
+
+    t, d = 2, 256
+    q = torch.zeros(t, 2, d, dtype=torch.bfloat16, device=dev)
+    kc = torch.zeros(4, 1, d, dtype=torch.float8_e4m3fn, device=dev)
+    cache = torch.zeros(8, d, device=dev)
+    pos = torch.zeros(t, dtype=torch.int64, device=dev)
+    assert not fused_qk_norm_rope_store_fp8(q, q[:, :1], q[:, :1], pos, pos, q[0, 0], q[0, 0],
+                                            1e-6, cache, kc, kc)
+
+
+def test_rope_inplace_matches_oracle(dev):
+    from flashrec_amd.kernel.sglops import apply_rope_inplace
+
+    t, hq, hk, d = 50, 16, 8, 128
+    g = torch.Generator().manual_seed(31)
+    q = torch.randn(t, hq * d, generator=g).to(torch.bfloat16)
+    k = torch.randn(t, hk * d, generator=g).to(torch.bfloat16)
+    cache = ops.cos_sin_cache(d, 1024, 1e6)
+    pos = torch.randint(0, 1024, (t,), generator=g)
+    qd, kd = q.to(dev), k.to(dev)
+    assert apply_rope_inplace(pos.to(dev), qd, kd, d, cache.to(dev))
+    q_ref = ops.apply_rope(pos, q.view(t, hq, d), cache).reshape(t, -1)
+    k_ref = ops.apply_rope(pos, k.view(t, hk, d), cache).reshape(t, -1)
+    assert torch.equal(qd.cpu().view(torch.int16), q_ref.view(torch.int16))
+    assert torch.equal(kd.cpu().view(torch.int16), k_ref.view(torch.int16))
+
+
+def test_store_kv_cache_bf16_and_fp8(dev):
+    from flashrec_amd.kernel.sglops import store_kv_cache
+
+    n, row = 100, 8 * 128
+    g = torch.Generator().manual_seed(41)
+    k = torch.randn(n, row, generator=g).to(torch.bfloat16)
+    v = torch.randn(n, row, generator=g).to(torch.bfloat16)
+    loc = torch.randperm(500, generator=g)[:n] + 1
+    kc = torch.zeros(501, row, dtype=torch.float8_e4m3fn, device=dev)
+    vc = torch.zeros_like(kc)
+    store_kv_cache(kc, vc, loc.to(dev), k.to(dev), v.to(dev))
+    kc_ref = torch.zeros(501, 8, 128, dtype=torch.float8_e4m3fn)
+    vc_ref = torch.zeros_like(kc_ref)
+    ops.store_kv(kc_ref, vc_ref, loc, k, v)
+    assert torch.equal(codes(kc), codes(kc_ref).reshape(501, row))
+    assert torch.equal(codes(vc), codes(vc_ref).reshape(501, row))
+    # fp8 rows are copied byte for byte
+    kc2 = torch.zeros_like(kc)
+    vc2 = torch.zeros_like(vc)
+    store_kv_cache(kc2, vc2, loc.to(dev), kc[loc.to(dev)], vc[loc.to(dev)])
+    assert torch.equal(codes(kc2), codes(kc))
+    assert torch.equal(codes(vc2), codes(vc))
+
+
+def test_out_of_range_slots_are_skipped(dev):
+    from flashrec_amd.kernel.sglops import store_kv_cache
+
+    k = torch.ones(3, 16, dtype=torch.bfloat16, device=dev)
+    loc = torch.tensor([1, -1, 99], device=dev)
+    kc = torch.zeros(4, 16, dtype=torch.float8_e4m3fn, device=dev)
+    vc = torch.zeros_like(kc)
+    store_kv_cache(kc, vc, loc, k, k)
+    c = codes(kc)
+    assert (c[1] == 0x38).all()  # e4m3(1.0)
+    assert (c[[0, 2, 3]] == 0).all()
