@@ -60,3 +60,23 @@ def max_abs_rel(got: torch.Tensor, ref: torch.Tensor) -> float:
     got = got.detach().cpu().float()
     ref = ref.detach().cpu().float()
     return ((got - ref).abs().max() / ref.abs().max().clamp(min=1e-30)).item()
+
+
+def assert_rope_parity(got, ref, n_ref, max_flip_frac=1e-3):
+    """Rotated heads (bf16 q, or decoded e4m3 K pages via ``decoded=True``
+    callers): bit-exact except where the per-head RMS normalisation flipped
+    one bf16 ULP (different fp32 summation order than torch's CPU).  Such a
+    flip moves an input of the rotation by <= 2^-8 |n|, so each output of the
+    pair (n_i, n_partner) may move by <= 2^-7 (|n_i| + |n_partner|)."""
+    got = got.detach().cpu().float()
+    ref = ref.detach().cpu().float()
+    n = n_ref.detach().cpu().float()
+    half = n.shape[-1] // 2
+    partner = torch.cat([n[..., half:], n[..., :half]], dim=-1)
+    bound = 2.0 ** -7 * (n.abs() + partner.abs())
+    diff = got != ref
+    frac = diff.float().mean().item()
+    assert frac < max_flip_frac, f"{frac:.2e} of rotated values differ"
+    if diff.any():
+        excess = ((got - ref).abs() - bound)[diff].max().item()
+        assert excess <= 0, f"rotated value off by {excess} beyond the one-ULP-norm-flip bound"

@@ -74,6 +74,8 @@ def test_per_token_quant_edge_rows(dev):
     x[4, ::2] = 448.0
     x[4, 1::2] = 464.0 * 448.0 / 464.0
     x[5] = torch.randn(1024, generator=torch.Generator().manual_seed(5)) * 1e-3
+    x[5, :64] = -0.0  # signed zeros keep their sign (code 0x80)
+    x[2, 100:110] = -0.0
     for dtype in (torch.float32, torch.bfloat16):
         xd = x.to(dtype)
         q, s = per_token_quant_fp8(xd.to(dev))

@@ -3,10 +3,25 @@
 import pytest
 import torch
 
-from helpers import assert_bf16_parity, code_flip_stats, codes
+from helpers import assert_bf16_parity, assert_rope_parity, code_flip_stats, codes
 from oracle import inputs, ops
 
 pytestmark = pytest.mark.gpu
+
+
+def _assert_k_pages(kc, kc_ref, k, kw, eps, loc):
+    """K pages: e4m3 of the rotated bf16 K.  Bytes equal except downstream of
+    a norm flip: then the decoded value may move by the rotation bound plus
+    one e4m3 step of either side."""
+    frac, _ = code_flip_stats(kc, kc_ref)
+    assert frac < 1e-3
+    got = kc.cpu().float()[loc]
+    ref = kc_ref.float()[loc]
+    n = ops.rmsnorm(k, kw, eps).float()
+    half = n.shape[-1] // 2
+    bound = 2.0 ** -7 * (n.abs() + torch.cat([n[..., half:], n[..., :half]], -1).abs())
+    bound = bound + 2.0 ** -3 * torch.maximum(got.abs(), ref.abs()) + 2.0 ** -9
+    assert ((got - ref).abs() <= bound).all()
 
 
 def _check(dev, q, k, v, pos, loc, qw, kw, eps, cache, slots, hk, d):
@@ -23,11 +38,10 @@ def _check(dev, q, k, v, pos, loc, qw, kw, eps, cache, slots, hk, d):
                                       eps, cache.to(dev), kc, vc)
     assert ok
     torch.cuda.synchronize()
-    assert_bf16_parity(qd, q_ref)
+    assert_rope_parity(qd, q_ref, ops.rmsnorm(q, qw, eps))
     # V: pure conversion + scatter, bit-exact including untouched slots
     assert torch.equal(codes(vc), codes(vc_ref))
-    frac, dist = code_flip_stats(kc, kc_ref)
-    assert dist <= 1 and frac < 1e-3
+    _assert_k_pages(kc, kc_ref, k, kw, eps, loc)
     # k and v inputs are not modified
     assert torch.equal(kd.cpu().view(torch.int16), k.view(torch.int16))
     return qd, kc, vc
@@ -84,10 +98,9 @@ def test_strided_views_of_fused_qkv(dev):
     assert fused_qk_norm_rope_store_fp8(qkv_d[:, :hq], qkv_d[:, hq:hq + hk], qkv_d[:, hq + hk:],
                                         pos.to(dev), loc.to(dev), w.to(dev), w.to(dev), 1e-6,
                                         cache.to(dev), kc, vc)
-    assert_bf16_parity(qkv_d[:, :hq], q_ref)
+    assert_rope_parity(qkv_d[:, :hq], q_ref, ops.rmsnorm(q, w, 1e-6))
     assert torch.equal(codes(vc), codes(vc_ref))
-    frac, dist = code_flip_stats(kc, kc_ref)
-    assert dist <= 1 and frac < 1e-3
+    _assert_k_pages(kc, kc_ref, k, w, 1e-6, loc)
 
 
 @pytest.mark.parametrize("hq,hk,d", [(6, 2, 64), (4, 4, 128), (3, 1, 100)])
