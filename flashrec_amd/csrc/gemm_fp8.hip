@@ -98,15 +98,27 @@ __device__ __forceinline__ void store4(void* out, int64_t ldo, int64_t m, int64_
   }
 }
 
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Raw buffer resource over [base, base + bytes): loads past the end return 0,
+// which zero-fills rows beyond M / N and the K tail without branches.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
 // BN: weight rows (output columns) per tile, BM: activation rows per tile.
-template <int BN, int BM, int OUT>
+// KTAIL: K is not a multiple of the 128-byte K tile (last tile zero-filled).
+template <int BN, int BM, int OUT, bool KTAIL>
 __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
+  // The host pass only needs the kernel's signature (for its launch stub);
+  // the body uses device-only buffer-resource builtins.
+#if defined(__HIP_DEVICE_COMPILE__)
   constexpr int FN = BN / 64;  // 32-row blocks per wave along n
   constexpr int FM = BM / 64;  // 32-row blocks per wave along m
-  constexpr int LB = BN / 32;  // 16-byte loads per thread for the weight tile
-  constexpr int LA = BM / 32;
+  constexpr int IB = BN / 32;  // 1 KB direct-to-LDS loads per wave per K tile (weights)
+  constexpr int IA = BM / 32;
   constexpr int STAGE = (BN + BM) * kBK;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -128,45 +140,38 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   const int64_t tn = (pid % width) / gsz;
   const int64_t n0 = tn * BN, m0 = tm * BM;
 
-  // ---- global load assignment: chunk c of rows r, r+32, ...
-  const int lc = tid & 7;
-  const int lr = tid >> 3;
-  const uint8_t* pb[LB];
-  const uint8_t* pa[LA];
-  bool vb[LB], va[LA];
+  // ---- direct-to-LDS loads.  One wave instruction fills 1 KB = 8 rows of
+  // 128 B; lane L lands in row L/8, chunk slot L%8, and therefore fetches the
+  // global chunk (L%8) ^ (L/8), which realises the XOR swizzle in LDS.
+  const __amdgpu_buffer_rsrc_t rb =
+      make_rsrc(g.b, static_cast<uint32_t>((g.N - 1) * g.ldb + g.K));
+  const __amdgpu_buffer_rsrc_t ra =
+      make_rsrc(g.a, static_cast<uint32_t>((g.M - 1) * g.lda + g.K));
+  const int lrow = lane >> 3;
+  const int lchunk = (lane & 7) ^ lrow;
+  uint32_t vob[IB], voa[IA];
 #pragma unroll
-  for (int i = 0; i < LB; ++i) {
-    const int64_t n = n0 + lr + 32 * i;
-    vb[i] = n < g.N;
-    pb[i] = g.b + (vb[i] ? n : 0) * g.ldb + lc * 16;
+  for (int i = 0; i < IB; ++i) {
+    const int64_t row = n0 + (i * 4 + wave) * 8 + lrow;
+    vob[i] = static_cast<uint32_t>(row * g.ldb + lchunk * 16);
   }
 #pragma unroll
-  for (int i = 0; i < LA; ++i) {
-    const int64_t m = m0 + lr + 32 * i;
-    va[i] = m < g.M;
-    pa[i] = g.a + (va[i] ? m : 0) * g.lda + lc * 16;
+  for (int i = 0; i < IA; ++i) {
+    const int64_t row = m0 + (i * 4 + wave) * 8 + lrow;
+    voa[i] = static_cast<uint32_t>(row * g.lda + lchunk * 16);
   }
-  u32x4 rb[LB], ra[LA];
-  auto gload = [&](int64_t k0) {
-    const bool kin = k0 + lc * 16 < g.K;
-#pragma unroll
-    for (int i = 0; i < LB; ++i) {
-      u32x4 z = {0u, 0u, 0u, 0u};
-      rb[i] = (vb[i] && kin) ? *reinterpret_cast<const u32x4*>(pb[i] + k0) : z;
-    }
-#pragma unroll
-    for (int i = 0; i < LA; ++i) {
-      u32x4 z = {0u, 0u, 0u, 0u};
-      ra[i] = (va[i] && kin) ? *reinterpret_cast<const u32x4*>(pa[i] + k0) : z;
-    }
-  };
-  auto sstore = [&](int stage) {
+  auto issue = [&](int stage, uint32_t k0) {
     uint8_t* sb = smem + stage * STAGE;
     uint8_t* sa = sb + BN * kBK;
+    const bool kin = !KTAIL || (k0 + lchunk * 16 < static_cast<uint64_t>(g.K));
 #pragma unroll
-    for (int i = 0; i < LB; ++i) *reinterpret_cast<u32x4*>(sb + swz(lr + 32 * i, lc)) = rb[i];
+    for (int i = 0; i < IB; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rb, (lds_ptr_t)(sb + (i * 4 + wave) * 1024), 16, kin ? vob[i] : 0x80000000u, k0, 0, 0);
 #pragma unroll
-    for (int i = 0; i < LA; ++i) *reinterpret_cast<u32x4*>(sa + swz(lr + 32 * i, lc)) = ra[i];
+    for (int i = 0; i < IA; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          ra, (lds_ptr_t)(sa + (i * 4 + wave) * 1024), 16, kin ? voa[i] : 0x80000000u, k0, 0, 0);
   };
 
   v16f acc[FN][FM];
@@ -177,17 +182,17 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  const int64_t KT = (g.K + kBK - 1) / kBK;
-  gload(0);
-  sstore(0);
+  const int KT = static_cast<int>((g.K + kBK - 1) / kBK);
+  issue(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  const int fr = lane & 31;         // fragment row inside a 32-row block
-  const int fk = (lane >> 5) * 2;   // first 16-byte chunk inside a 64-byte K chunk
+  const int fr = lane & 31;        // fragment row inside a 32-row block
+  const int fk = (lane >> 5) * 2;  // first 16-byte chunk inside a 64-byte K chunk
 
-  for (int64_t kt = 0; kt < KT; ++kt) {
-    const int cur = static_cast<int>(kt & 1);
-    if (kt + 1 < KT) gload((kt + 1) * kBK);
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < KT) issue(cur ^ 1, static_cast<uint32_t>(kt + 1) * kBK);
     const uint8_t* sb = smem + cur * STAGE;
     const uint8_t* sa = sb + BN * kBK;
 #pragma unroll
@@ -217,24 +222,47 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
           acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[i], fa[j], acc[i][j], 0, 0,
                                                                      0, 0, 0, 0);
     }
-    if (kt + 1 < KT) sstore(cur ^ 1);
-    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of the next tile have landed
+    __syncthreads();                 // ... and everyone's; the current tile is free
   }
 
   // ---- epilogue: lane holds, per block (i, j), column m = l%32 and the
   // four consecutive rows n = 8*q + 4*(l/32) + 0..3 for q = 0..3.
+  const bool full = m0 + BM <= g.M && n0 + BN <= g.N && (g.ldo & 3) == 0 && g.bias == nullptr;
 #pragma unroll
   for (int j = 0; j < FM; ++j) {
     const int64_t m = m0 + wm * (BM / 2) + j * 32 + (lane & 31);
-    if (m >= g.M) continue;
+    if (!full && m >= g.M) continue;
     const float sam = g.sa[m * g.sa_stride];
 #pragma unroll
     for (int i = 0; i < FN; ++i) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int64_t n = n0 + wn * (BN / 2) + i * 32 + 8 * q + 4 * (lane >> 5);
-        if (n >= g.N) continue;
         float v[4];
+        if (full) {
+          if (g.sb_stride) {
+            const float4 sbv = *reinterpret_cast<const float4*>(g.sb + n);
+            v[0] = (acc[i][j][4 * q + 0] * sam) * sbv.x;
+            v[1] = (acc[i][j][4 * q + 1] * sam) * sbv.y;
+            v[2] = (acc[i][j][4 * q + 2] * sam) * sbv.z;
+            v[3] = (acc[i][j][4 * q + 3] * sam) * sbv.w;
+          } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) v[t] = (acc[i][j][4 * q + t] * sam) * g.sb[0];
+          }
+          if (OUT == FR_DTYPE_FP32) {
+            *reinterpret_cast<float4*>(static_cast<float*>(g.out) + m * g.ldo + n) =
+                make_float4(v[0], v[1], v[2], v[3]);
+          } else {
+            u32x2 w;
+            w[0] = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v[0], v[1]) : pack_fp16x2(v[0], v[1]);
+            w[1] = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v[2], v[3]) : pack_fp16x2(v[2], v[3]);
+            *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(g.out) + m * g.ldo + n) = w;
+          }
+          continue;
+        }
+        if (n >= g.N) continue;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const int64_t nn = n + t < g.N ? n + t : g.N - 1;
@@ -244,6 +272,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
       }
     }
   }
+#endif  // __HIP_DEVICE_COMPILE__
 }
 
 // Scalar fallback for shapes/strides the MFMA kernel does not take
@@ -266,16 +295,23 @@ __global__ __launch_bounds__(256) void gemm_fp8_scalar(GemmArgs g) {
 template <int BN, int BM, int OUT>
 static hipError_t launch_mfma(const GemmArgs& g, hipStream_t st) {
   const int64_t nt = ((g.N + BN - 1) / BN) * ((g.M + BM - 1) / BM);
-  hipLaunchKernelGGL((gemm_fp8_mfma<BN, BM, OUT>), dim3(static_cast<unsigned>(nt)), dim3(256), 0,
-                     st, g);
+  if (g.K % kBK == 0)
+    hipLaunchKernelGGL((gemm_fp8_mfma<BN, BM, OUT, false>), dim3(static_cast<unsigned>(nt)),
+                       dim3(256), 0, st, g);
+  else
+    hipLaunchKernelGGL((gemm_fp8_mfma<BN, BM, OUT, true>), dim3(static_cast<unsigned>(nt)),
+                       dim3(256), 0, st, g);
   return hipGetLastError();
 }
 
 template <int OUT>
 static hipError_t dispatch(const GemmArgs& g, hipStream_t st) {
   auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-  const bool mfma_ok = g.K % 16 == 0 && g.lda % 16 == 0 && g.ldb % 16 == 0 && al16(g.a) &&
-                       al16(g.b);
+  // Buffer offsets are 32-bit: each operand must span < 2 GiB; the K == 0
+  // case has nothing to load.
+  const bool mfma_ok = g.K > 0 && g.K % 16 == 0 && g.lda % 16 == 0 && g.ldb % 16 == 0 &&
+                       al16(g.a) && al16(g.b) && (g.M - 1) * g.lda + g.K < (int64_t(1) << 31) &&
+                       (g.N - 1) * g.ldb + g.K < (int64_t(1) << 31);
   if (!mfma_ok) {
     const int64_t total = g.M * g.N;
     hipLaunchKernelGGL((gemm_fp8_scalar<OUT>), dim3(static_cast<unsigned>((total + 255) / 256)),
