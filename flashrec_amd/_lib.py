@@ -15,7 +15,7 @@ from typing import Optional
 
 import torch
 
-LIB_PATH = Path(os.environ.get("FLASHREC_AMD_LIB", Path(__file__).resolve().parent / "libflashrec_amd.so"))
+LIB_PATH = Path(os.environ.get("FLASHREC_AMD_LIB") or Path(__file__).resolve().parent / "libflashrec_amd.so")
 
 FR_OK = 0
 FR_EINVAL = 1

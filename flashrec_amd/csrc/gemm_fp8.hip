@@ -7,31 +7,34 @@
 // from python/flashrec/layers/linear.py:153-172.
 //
 // Design (gfx950):
-//  * 256 threads = 4 wave64 in a 2x2 grid; each wave owns a
-//    (BN/2) x (BM/2) sub-tile built from 32x32 blocks of
-//    v_mfma_f32_32x32x64_f8f6f4 (A-operand = weight rows, B-operand =
-//    activation rows, so every lane ends up holding 4 consecutive output
-//    columns and stores 8 bytes at a time).
-//  * K is consumed in 128-byte tiles staged through LDS, double buffered:
-//    the next tile's global loads are in flight while the current one feeds
-//    the MFMAs, one barrier per K tile.
-//  * LDS rows are 128 bytes (8 chunks of 16 B); chunk c of row r lives at
-//    chunk slot c ^ (r & 7), so the 16-byte fragment reads of 8 consecutive
-//    rows hit 8 distinct bank groups (conflict free) and the 16-byte writes
-//    of one row stay conflict free as well.
-//  * The MFMA's K ordering inside one instruction is irrelevant as long as
-//    both operands use the same (lane group, byte) -> k assignment: lane l
-//    supplies row l%32 and the 32 contiguous bytes k0 + (l/32)*32 .. +31 of
-//    the current 64-byte K chunk for both operands.
+//  * Persistent: one 256-thread workgroup per CU walks its share of the
+//    output tiles.  The K steps of consecutive tiles form one continuous
+//    stream, so the direct-to-LDS loads for the next tile's first K steps
+//    are in flight while the current tile finishes and stores its output.
+//  * 4 wave64 in a 2x2 grid; each wave owns a (BN/2) x (BM/2) sub-tile of
+//    32x32 blocks of v_mfma_f32_32x32x64_f8f6f4 (A-operand = weight rows,
+//    B-operand = activation rows).  The K order inside one MFMA does not
+//    matter as long as both operands use the same (lane group, byte) -> k
+//    assignment: lane l supplies row l%32 and bytes (l/32)*32 .. +31 of the
+//    64-byte K step, for both operands.
+//  * K is consumed in 64-byte steps through an NST-slot LDS ring filled by
+//    buffer_load ... lds (no VGPR staging; rows past M/N and the K tail read
+//    as zero through the buffer range check).  One barrier per step.
+//  * Fragments of step s+1 are read from LDS while the last MFMAs of step s
+//    run (register double buffering).
+//  * Epilogue: scales applied in fp32, converted, transposed through a
+//    separate 8 KB-per-wave LDS staging area and written as full 256-byte
+//    row segments (16 lanes x 16 B), instead of scattered 8-byte pieces.
 //  * Workgroup -> tile mapping is XCD aware: dispatch places workgroup i on
-//    XCD i % 8, so consecutive tiles (which share weight/activation panels)
-//    are given to workgroups on the same XCD and its L2.
+//    XCD i % 8; tiles are renumbered so each XCD walks a contiguous, m-grouped
+//    range and its 32 CUs share weight/activation panels in their L2.
 #include "fr_common.h"
 
 namespace fr {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 struct GemmArgs {
   const uint8_t* a;
@@ -48,10 +51,52 @@ struct GemmArgs {
   int64_t M, N, K;
 };
 
-constexpr int kBK = 128;  // bytes of K per LDS tile
+constexpr int kBK = 64;  // bytes of K per LDS step (one MFMA K step)
 
-__device__ __forceinline__ int swz(int r, int c) { return (r * 8 + (c ^ (r & 7))) * 16; }
+// LDS rows are 64 bytes (4 chunks of 16 B); chunk c of row r lives in slot
+// c ^ g(r) with g(r) = r2 | (r1 ^ r3) << 1 (r_i = bit i of r).  For the
+// 16-byte fragment reads (lane l reads row l % 32) this spreads every group
+// of 8 consecutive rows over the 8 distinct 16-byte bank groups of a
+// 128-byte bank line, and every group of 16 rows over the 16 of a 256-byte
+// line, so the reads are conflict free whether the LDS serves 128 or 256
+// bytes per clock.
+__device__ __forceinline__ int swz_g(int r) {
+  return ((r >> 2) & 1) | ((((r >> 1) ^ (r >> 3)) & 1) << 1);
+}
+__device__ __forceinline__ int swz(int r, int c) { return r * 64 + ((c ^ swz_g(r)) << 4); }
 
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() would
+// also wait for every outstanding global->LDS load (vmcnt(0)) and so drain
+// the prefetch ring; the explicit waitcnt_vm<> calls do that part.  The asm
+// memory clobber keeps the compiler from moving memory accesses across it,
+// lgkmcnt(0) retires this wave's LDS reads first (no wave can then overwrite
+// a slot another wave is still reading), and sched_barrier(0) pins every
+// other instruction to its side.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
+template <int N>
+__device__ __forceinline__ void waitcnt_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Raw buffer resource over [base, base + bytes): loads past the end return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
+template <int OUT>
+struct OutT {
+  static constexpr int kBytes = OUT == FR_DTYPE_FP32 ? 4 : 2;
+};
+
+// Four consecutive outputs of one row, with optional bias, bounds-checked.
 template <int OUT>
 __device__ __forceinline__ void store4(void* out, int64_t ldo, int64_t m, int64_t n, int64_t N,
                                        const float* v, const void* bias) {
@@ -63,12 +108,8 @@ __device__ __forceinline__ void store4(void* out, int64_t ldo, int64_t m, int64_
       for (int i = 0; i < 4; ++i)
         if (n + i < N) t[i] += bb[i];
     }
-    if (n + 3 < N && (ldo & 3) == 0) {
-      *reinterpret_cast<float4*>(o) = make_float4(t[0], t[1], t[2], t[3]);
-    } else {
-      for (int i = 0; i < 4; ++i)
-        if (n + i < N) o[i] = t[i];
-    }
+    for (int i = 0; i < 4; ++i)
+      if (n + i < N) o[i] = t[i];
     return;
   }
   uint16_t* o = static_cast<uint16_t*>(out) + m * ldo + n;
@@ -77,201 +118,341 @@ __device__ __forceinline__ void store4(void* out, int64_t ldo, int64_t m, int64_
     for (int i = 0; i < 4; ++i)
       if (n + i < N) t[i] += (OUT == FR_DTYPE_BF16) ? bf16_to_f32(bb[i]) : fp16_to_f32(bb[i]);
   }
-  uint32_t lo, hi;
-  if (OUT == FR_DTYPE_BF16) {
-    lo = pack_bf16x2(t[0], t[1]);
-    hi = pack_bf16x2(t[2], t[3]);
-  } else {
-    lo = pack_fp16x2(t[0], t[1]);
-    hi = pack_fp16x2(t[2], t[3]);
-  }
-  if (n + 3 < N && (ldo & 3) == 0) {
-    u32x2 w;
-    w[0] = lo;
-    w[1] = hi;
-    *reinterpret_cast<u32x2*>(o) = w;
-  } else {
-    uint16_t h[4] = {(uint16_t)(lo & 0xFFFF), (uint16_t)(lo >> 16), (uint16_t)(hi & 0xFFFF),
-                     (uint16_t)(hi >> 16)};
-    for (int i = 0; i < 4; ++i)
-      if (n + i < N) o[i] = h[i];
-  }
+  uint32_t lo = OUT == FR_DTYPE_BF16 ? pack_bf16x2(t[0], t[1]) : pack_fp16x2(t[0], t[1]);
+  uint32_t hi = OUT == FR_DTYPE_BF16 ? pack_bf16x2(t[2], t[3]) : pack_fp16x2(t[2], t[3]);
+  uint16_t h[4] = {(uint16_t)(lo & 0xFFFF), (uint16_t)(lo >> 16), (uint16_t)(hi & 0xFFFF),
+                   (uint16_t)(hi >> 16)};
+  for (int i = 0; i < 4; ++i)
+    if (n + i < N) o[i] = h[i];
 }
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-// Raw buffer resource over [base, base + bytes): loads past the end return 0,
-// which zero-fills rows beyond M / N and the K tail without branches.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+// Logical tile id -> (tm, tn): XCD-aware renumbering (workgroup i runs on XCD
+// i % 8 and, being persistent, only ever sees ids == i mod 8), then groups of
+// kGroupM m-tiles walked n-major so concurrent tiles share panels.
+__device__ __forceinline__ void tile_coords(int64_t pid, int64_t nt, int64_t tilesM, int64_t& tm,
+                                            int64_t& tn) {
+  if ((nt & 7) == 0) pid = (pid & 7) * (nt >> 3) + (pid >> 3);
+  constexpr int64_t kGroupM = 8;
+  const int64_t tilesN = nt / tilesM;
+  const int64_t width = kGroupM * tilesN;
+  const int64_t gid = pid / width;
+  const int64_t first_m = gid * kGroupM;
+  const int64_t gsz = (tilesM - first_m) < kGroupM ? (tilesM - first_m) : kGroupM;
+  tm = first_m + (pid % width) % gsz;
+  tn = (pid % width) / gsz;
 }
 
-// BN: weight rows (output columns) per tile, BM: activation rows per tile.
-// KTAIL: K is not a multiple of the 128-byte K tile (last tile zero-filled).
-template <int BN, int BM, int OUT, bool KTAIL>
+// BN: weight rows (output columns) per tile, BM: activation rows per tile,
+// NST: LDS ring depth in 64-byte K steps, KTAIL: K % 128 != 0 (the last
+// K steps are partly or wholly zero-filled).
+template <int BN, int BM, int NST, int OUT, bool KTAIL>
 __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   // The host pass only needs the kernel's signature (for its launch stub);
   // the body uses device-only buffer-resource builtins.
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int FN = BN / 64;  // 32-row blocks per wave along n
   constexpr int FM = BM / 64;  // 32-row blocks per wave along m
-  constexpr int IB = BN / 32;  // 1 KB direct-to-LDS loads per wave per K tile (weights)
-  constexpr int IA = BM / 32;
+  constexpr int WN = BN / 2;   // wave sub-tile: WN output columns ...
+  constexpr int WM = BM / 2;   // ... x WM output rows
+  constexpr int IB = BN / 64;  // 1 KB direct-to-LDS loads per wave per K step (weights)
+  constexpr int IA = BM / 64;  // ... (activations)
   constexpr int STAGE = (BN + BM) * kBK;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+  constexpr int LOADS = IB + IA;  // vmcnt units one K step adds per wave
+  constexpr int EB = OutT<OUT>::kBytes;
+  constexpr int STG = 32 * 256;  // epilogue staging per wave: 32 rows x 64 fp32
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * STAGE + 4 * STG];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // wave index in an SGPR: LDS destinations (M0) and row bases are scalar
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wn = wave & 1, wm = wave >> 1;
 
-  // ---- tile index: XCD-aware remap, then grouped ordering along m.
   const int64_t tilesN = (g.N + BN - 1) / BN;
   const int64_t tilesM = (g.M + BM - 1) / BM;
   const int64_t nt = tilesN * tilesM;
-  int64_t pid = blockIdx.x;
-  if ((nt & 7) == 0) pid = (pid & 7) * (nt >> 3) + (pid >> 3);
-  constexpr int64_t kGroupM = 8;
-  const int64_t width = kGroupM * tilesN;
-  const int64_t gid = pid / width;
-  const int64_t first_m = gid * kGroupM;
-  const int64_t gsz = (tilesM - first_m) < kGroupM ? (tilesM - first_m) : kGroupM;
-  const int64_t tm = first_m + (pid % width) % gsz;
-  const int64_t tn = (pid % width) / gsz;
-  const int64_t n0 = tn * BN, m0 = tm * BM;
+  const int64_t G = gridDim.x;
+  const int64_t my_tiles = (nt - blockIdx.x + G - 1) / G;
+  // K steps per tile, rounded up to even (steps run in pairs); steps past
+  // K read zeros through the buffer range check.
+  const int KT = static_cast<int>((g.K + 2 * kBK - 1) / (2 * kBK)) * 2;
+  const int64_t S = my_tiles * KT;  // K steps this workgroup runs
+  if (S == 0) return;
 
-  // ---- direct-to-LDS loads.  One wave instruction fills 1 KB = 8 rows of
-  // 128 B; lane L lands in row L/8, chunk slot L%8, and therefore fetches the
-  // global chunk (L%8) ^ (L/8), which realises the XOR swizzle in LDS.
   const __amdgpu_buffer_rsrc_t rb =
       make_rsrc(g.b, static_cast<uint32_t>((g.N - 1) * g.ldb + g.K));
   const __amdgpu_buffer_rsrc_t ra =
       make_rsrc(g.a, static_cast<uint32_t>((g.M - 1) * g.lda + g.K));
-  const int lrow = lane >> 3;
-  const int lchunk = (lane & 7) ^ lrow;
-  uint32_t vob[IB], voa[IA];
+
+  // ---- direct-to-LDS loads.  One wave instruction fills 1 KB = 16 rows of
+  // 64 B; lane L lands in row L/4, chunk slot L%4, so it fetches the global
+  // chunk (L%4) ^ g(L/4).  Per-lane row offsets are kept for the tile being
+  // computed (cur) and the next one (nxt): the ring runs NST steps ahead, so
+  // the last NST steps of a tile load the first ones of the next.  Offsets of
+  // a tile past the end are out of range (loads return zeros, touch nothing).
+  const int lrow = lane >> 2;
+  const int lchunk = (lane & 3) ^ swz_g(lrow);
+  constexpr uint32_t kOOB = 0x80000000u;
+  uint32_t ob_cur[IB], oa_cur[IA], ob_nxt[IB], oa_nxt[IA];
+  auto tile_offsets = [&](int64_t local, uint32_t* ob, uint32_t* oa) __attribute__((always_inline)) {
+    if (local >= my_tiles) {
 #pragma unroll
-  for (int i = 0; i < IB; ++i) {
-    const int64_t row = n0 + (i * 4 + wave) * 8 + lrow;
-    vob[i] = static_cast<uint32_t>(row * g.ldb + lchunk * 16);
-  }
+      for (int i = 0; i < IB; ++i) ob[i] = kOOB;
 #pragma unroll
-  for (int i = 0; i < IA; ++i) {
-    const int64_t row = m0 + (i * 4 + wave) * 8 + lrow;
-    voa[i] = static_cast<uint32_t>(row * g.lda + lchunk * 16);
-  }
-  auto issue = [&](int stage, uint32_t k0) {
-    uint8_t* sb = smem + stage * STAGE;
-    uint8_t* sa = sb + BN * kBK;
-    const bool kin = !KTAIL || (k0 + lchunk * 16 < static_cast<uint64_t>(g.K));
+      for (int i = 0; i < IA; ++i) oa[i] = kOOB;
+      return;
+    }
+    int64_t tm, tn;
+    tile_coords(blockIdx.x + local * G, nt, tilesM, tm, tn);
 #pragma unroll
     for (int i = 0; i < IB; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rb, (lds_ptr_t)(sb + (i * 4 + wave) * 1024), 16, kin ? vob[i] : 0x80000000u, k0, 0, 0);
+      ob[i] = static_cast<uint32_t>((tn * BN + (i * 4 + wave) * 16 + lrow) * g.ldb + lchunk * 16);
 #pragma unroll
     for (int i = 0; i < IA; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          ra, (lds_ptr_t)(sa + (i * 4 + wave) * 1024), 16, kin ? voa[i] : 0x80000000u, k0, 0, 0);
+      oa[i] = static_cast<uint32_t>((tm * BM + (i * 4 + wave) * 16 + lrow) * g.lda + lchunk * 16);
+  };
+  // Loads of K step `lk` (0..KT-1) of the cur or nxt tile into `slot`.
+  auto issue = [&](int slot, int lk, bool next) __attribute__((always_inline)) {
+    uint8_t* sb = smem + slot * STAGE;
+    uint8_t* sa = sb + BN * kBK;
+    const uint32_t k0 = static_cast<uint32_t>(lk) * kBK;
+    const bool kin = !KTAIL || (k0 + lchunk * 16 < static_cast<uint64_t>(g.K));
+#pragma unroll
+    for (int i = 0; i < IB; ++i) {
+      const uint32_t o = next ? ob_nxt[i] : ob_cur[i];
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(sb + (i * 4 + wave) * 1024), 16,
+                                               kin ? o : kOOB, k0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < IA; ++i) {
+      const uint32_t o = next ? oa_nxt[i] : oa_cur[i];
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(sa + (i * 4 + wave) * 1024), 16,
+                                               kin ? o : kOOB, k0, 0, 0);
+    }
   };
 
-  v16f acc[FN][FM];
-#pragma unroll
-  for (int i = 0; i < FN; ++i)
-#pragma unroll
-    for (int j = 0; j < FM; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-
-  const int KT = static_cast<int>((g.K + kBK - 1) / kBK);
-  issue(0, 0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-
+  // ---- fragments and MFMAs
   const int fr = lane & 31;        // fragment row inside a 32-row block
-  const int fk = (lane >> 5) * 2;  // first 16-byte chunk inside a 64-byte K chunk
-
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < KT) issue(cur ^ 1, static_cast<uint32_t>(kt + 1) * kBK);
-    const uint8_t* sb = smem + cur * STAGE;
+  const int c0 = (lane >> 5) * 2;  // first 16-byte chunk of this lane's 32 bytes
+  struct Frags {
+    v8i b[FN], a[FM];
+  };
+  auto read_frags = [&](Frags& f, int slot) __attribute__((always_inline)) {
+    const uint8_t* sb = smem + slot * STAGE;
     const uint8_t* sa = sb + BN * kBK;
 #pragma unroll
-    for (int kc = 0; kc < 2; ++kc) {
-      v8i fb[FN], fa[FM];
-      const int c0 = kc * 4 + fk;
+    for (int i = 0; i < FN; ++i) {
+      const int r = wn * WN + i * 32 + fr;
+      u32x4 x0 = *reinterpret_cast<const u32x4*>(sb + swz(r, c0));
+      u32x4 x1 = *reinterpret_cast<const u32x4*>(sb + swz(r, c0 + 1));
+      f.b[i] = v8i{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3],
+                   (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+    }
 #pragma unroll
-      for (int i = 0; i < FN; ++i) {
-        const int r = wn * (BN / 2) + i * 32 + fr;
-        u32x4 x0 = *reinterpret_cast<const u32x4*>(sb + swz(r, c0));
-        u32x4 x1 = *reinterpret_cast<const u32x4*>(sb + swz(r, c0 + 1));
-        fb[i] = v8i{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3],
-                    (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+    for (int j = 0; j < FM; ++j) {
+      const int r = wm * WM + j * 32 + fr;
+      u32x4 x0 = *reinterpret_cast<const u32x4*>(sa + swz(r, c0));
+      u32x4 x1 = *reinterpret_cast<const u32x4*>(sa + swz(r, c0 + 1));
+      f.a[j] = v8i{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3],
+                   (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+    }
+  };
+  v16f acc[FN][FM];
+  auto zero_acc = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+  };
+  auto mfma_rows = [&](const Frags& f, int i0, int i1) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = i0; i < i1; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.b[i], f.a[j], acc[i][j], 0,
+                                                                   0, 0, 0, 0, 0);
+  };
+
+  // ---- epilogue of one tile.  Lane l holds, per block (i, j), output row
+  // m = l%32 of block j and the 4 consecutive columns n = 8q + 4(l/32) + t of
+  // block i (q, t = 0..3).  Fast path: acc * sa[m] goes to an fp32 staging
+  // tile of 32 rows x 64 columns per pass (16-byte chunk c of row r at slot
+  // c ^ (r % 16)), is read back as 8 consecutive columns per lane, multiplied
+  // by sb[n], converted and stored as whole row segments.  The scales of the
+  // tile are loaded into registers when the tile starts (load_scales), so the
+  // epilogue issues no global load: any load here would have to wait behind
+  // the next tile's ring loads (vmcnt retires in order).
+  constexpr int PCOLS = 64;                          // fp32 staging columns per pass
+  constexpr int PASSES = WN / PCOLS;
+  static_assert(WN % PCOLS == 0, "wave tile width");
+  uint8_t* stg = smem + NST * STAGE + wave * STG;
+  float sa_r[FM];
+  float sb_r[PASSES][8];
+  auto load_scales = [&](int64_t local) __attribute__((always_inline)) {
+    if (local >= my_tiles) return;
+    int64_t tm, tn;
+    tile_coords(blockIdx.x + local * G, nt, tilesM, tm, tn);
+    const int64_t m0 = tm * BM + wm * WM;
+    const int64_t n0 = tn * BN + wn * WN;
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+      int64_t m = m0 + j * 32 + (lane & 31);
+      m = m < g.M ? m : g.M - 1;
+      sa_r[j] = g.sa[m * g.sa_stride];
+    }
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        int64_t n = n0 + p * PCOLS + (lane & 7) * 8 + t;
+        n = n < g.N ? n : g.N - 1;
+        sb_r[p][t] = g.sb[n * g.sb_stride];
       }
+  };
+  auto epilogue = [&](int64_t local) __attribute__((always_inline)) {
+    int64_t tm, tn;
+    tile_coords(blockIdx.x + local * G, nt, tilesM, tm, tn);
+    const int64_t m0 = tm * BM + wm * WM;
+    const int64_t n0 = tn * BN + wn * WN;
+    const bool fast = tm * BM + BM <= g.M && tn * BN + BN <= g.N && g.bias == nullptr &&
+                      (g.ldo * EB) % 16 == 0 && (reinterpret_cast<uintptr_t>(g.out) & 15) == 0;
+    if (!fast) {
 #pragma unroll
       for (int j = 0; j < FM; ++j) {
-        const int r = wm * (BM / 2) + j * 32 + fr;
-        u32x4 x0 = *reinterpret_cast<const u32x4*>(sa + swz(r, c0));
-        u32x4 x1 = *reinterpret_cast<const u32x4*>(sa + swz(r, c0 + 1));
-        fa[j] = v8i{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3],
-                    (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
-      }
+        const int64_t m = m0 + j * 32 + (lane & 31);
+        if (m >= g.M) continue;
+        const float sam = g.sa[m * g.sa_stride];
 #pragma unroll
-      for (int i = 0; i < FN; ++i)
+        for (int i = 0; i < FN; ++i)
 #pragma unroll
-        for (int j = 0; j < FM; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[i], fa[j], acc[i][j], 0, 0,
-                                                                     0, 0, 0, 0);
-    }
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of the next tile have landed
-    __syncthreads();                 // ... and everyone's; the current tile is free
-  }
-
-  // ---- epilogue: lane holds, per block (i, j), column m = l%32 and the
-  // four consecutive rows n = 8*q + 4*(l/32) + 0..3 for q = 0..3.
-  const bool full = m0 + BM <= g.M && n0 + BN <= g.N && (g.ldo & 3) == 0 && g.bias == nullptr;
+          for (int q = 0; q < 4; ++q) {
+            const int64_t n = n0 + i * 32 + 8 * q + 4 * (lane >> 5);
+            if (n >= g.N) continue;
+            float v[4];
 #pragma unroll
-  for (int j = 0; j < FM; ++j) {
-    const int64_t m = m0 + wm * (BM / 2) + j * 32 + (lane & 31);
-    if (!full && m >= g.M) continue;
-    const float sam = g.sa[m * g.sa_stride];
-#pragma unroll
-    for (int i = 0; i < FN; ++i) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int64_t n = n0 + wn * (BN / 2) + i * 32 + 8 * q + 4 * (lane >> 5);
-        float v[4];
-        if (full) {
-          if (g.sb_stride) {
-            const float4 sbv = *reinterpret_cast<const float4*>(g.sb + n);
-            v[0] = (acc[i][j][4 * q + 0] * sam) * sbv.x;
-            v[1] = (acc[i][j][4 * q + 1] * sam) * sbv.y;
-            v[2] = (acc[i][j][4 * q + 2] * sam) * sbv.z;
-            v[3] = (acc[i][j][4 * q + 3] * sam) * sbv.w;
-          } else {
-#pragma unroll
-            for (int t = 0; t < 4; ++t) v[t] = (acc[i][j][4 * q + t] * sam) * g.sb[0];
+            for (int t = 0; t < 4; ++t) {
+              const int64_t nn = n + t < g.N ? n + t : g.N - 1;
+              v[t] = (acc[i][j][4 * q + t] * sam) * g.sb[nn * g.sb_stride];
+            }
+            store4<OUT>(g.out, g.ldo, m, n, g.N, v, g.bias);
           }
+      }
+      return;
+    }
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+#pragma unroll
+      for (int p = 0; p < PASSES; ++p) {
+        const int row = lane & 31;
+#pragma unroll
+        for (int ii = 0; ii < PCOLS / 32; ++ii) {
+          const int i = p * (PCOLS / 32) + ii;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int chunk = ii * 8 + 2 * q + (lane >> 5);  // 16-byte chunk of the pass row
+            float4 v = make_float4(acc[i][j][4 * q + 0] * sa_r[j], acc[i][j][4 * q + 1] * sa_r[j],
+                                   acc[i][j][4 * q + 2] * sa_r[j], acc[i][j][4 * q + 3] * sa_r[j]);
+            *reinterpret_cast<float4*>(stg + row * 256 + ((chunk ^ (row & 15)) << 4)) = v;
+          }
+        }
+        // read back: 8 lanes per row, 8 consecutive columns per lane
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int r = rr * 8 + (lane >> 3);
+          const int cg = lane & 7;
+          const float4 x0 =
+              *reinterpret_cast<const float4*>(stg + r * 256 + (((2 * cg) ^ (r & 15)) << 4));
+          const float4 x1 =
+              *reinterpret_cast<const float4*>(stg + r * 256 + (((2 * cg + 1) ^ (r & 15)) << 4));
+          const float v[8] = {x0.x * sb_r[p][0], x0.y * sb_r[p][1], x0.z * sb_r[p][2],
+                              x0.w * sb_r[p][3], x1.x * sb_r[p][4], x1.y * sb_r[p][5],
+                              x1.z * sb_r[p][6], x1.w * sb_r[p][7]};
+          const int64_t off = (m0 + j * 32 + r) * g.ldo + n0 + p * PCOLS + cg * 8;
           if (OUT == FR_DTYPE_FP32) {
-            *reinterpret_cast<float4*>(static_cast<float*>(g.out) + m * g.ldo + n) =
-                make_float4(v[0], v[1], v[2], v[3]);
+            float* o = static_cast<float*>(g.out) + off;
+            *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
+            *reinterpret_cast<float4*>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
           } else {
-            u32x2 w;
-            w[0] = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v[0], v[1]) : pack_fp16x2(v[0], v[1]);
-            w[1] = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v[2], v[3]) : pack_fp16x2(v[2], v[3]);
-            *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(g.out) + m * g.ldo + n) = w;
-          }
-          continue;
-        }
-        if (n >= g.N) continue;
+            u32x4 w;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const int64_t nn = n + t < g.N ? n + t : g.N - 1;
-          v[t] = (acc[i][j][4 * q + t] * sam) * g.sb[nn * g.sb_stride];
+            for (int t = 0; t < 4; ++t)
+              w[t] = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v[2 * t], v[2 * t + 1])
+                                          : pack_fp16x2(v[2 * t], v[2 * t + 1]);
+            *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(g.out) + off) = w;
+          }
         }
-        store4<OUT>(g.out, g.ldo, m, n, g.N, v, g.bias);
       }
     }
+  };
+
+  // ---- prologue: the first NST steps in flight; all but the last landed.
+  // With more than one tile per workgroup KT >= NST (see launch_mfma), so
+  // the prologue stays inside tile 0; with one tile, steps past its end are
+  // all-zero dummies.
+  tile_offsets(0, ob_cur, oa_cur);
+  tile_offsets(1, ob_nxt, oa_nxt);
+  load_scales(0);
+#pragma unroll
+  for (int st = 0; st < NST; ++st) issue(st, st < KT ? st : st - KT, st >= KT);
+  waitcnt_vm<LOADS>();
+  lds_barrier();
+  zero_acc();
+  Frags f0, f1;
+  read_frags(f0, 0);
+
+  // ---- main loop.  Step s (tile s / KT, K step kt = s % KT) holds its
+  // fragments in `cur`: multiply all but the last weight block row; wait for
+  // step s+1 (own loads, then everyone's through the barrier, which also
+  // retires every wave's reads of slot s % NST); refill that slot with step
+  // s+NST; read step s+1's fragments into `nxt` while the last row's MFMAs
+  // run.  Every step has the same shape: past the end the ring loads zeros
+  // and the last fragment read is discarded.
+  //
+  // vmcnt retires loads in order but counts stores too, so a load wait issued
+  // while the epilogue's stores are in flight would also wait for them.
+  // Hence, before a tile's epilogue every ring load but the newest step's is
+  // drained (waitcnt_vm<LOADS>), and the first two steps of the next tile
+  // (whose data needs only those loads) skip the vmcnt wait: the stores get
+  // two steps to complete before the next load wait.  Requires NST >= 4.
+  static_assert(NST >= 4, "two wait-free steps need a 4-deep ring");
+  auto step = [&](Frags& cur, Frags& nxt, int64_t s, int kt, bool wait)
+      __attribute__((always_inline)) {
+    mfma_rows(cur, 0, FN - 1);
+    if (wait) waitcnt_vm<(NST - 2) * LOADS>();
+    lds_barrier();
+    const int lk = kt + NST;
+    issue(static_cast<int>(s % NST), lk < KT ? lk : lk - KT, lk >= KT);
+    read_frags(nxt, static_cast<int>((s + 1) % NST));
+    mfma_rows(cur, FN - 1, FN);
+    __builtin_amdgcn_sched_group_barrier(0x020, LOADS, 0);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * (FN + FM) / FM, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
+  };
+  int64_t s = 0;
+  for (int64_t tile = 0; tile < my_tiles; ++tile) {
+    step(f0, f1, s, 0, false);
+    step(f1, f0, s + 1, 1, false);
+    s += 2;
+    for (int kt = 2; kt < KT; kt += 2, s += 2) {  // KT is even
+      step(f0, f1, s, kt, true);
+      step(f1, f0, s + 1, kt + 1, true);
+    }
+    waitcnt_vm<LOADS>();
+    epilogue(tile);
+    zero_acc();
+    load_scales(tile + 1);
+#pragma unroll
+    for (int i = 0; i < IB; ++i) ob_cur[i] = ob_nxt[i];
+#pragma unroll
+    for (int i = 0; i < IA; ++i) oa_cur[i] = oa_nxt[i];
+    tile_offsets(tile + 2, ob_nxt, oa_nxt);
   }
+  waitcnt_vm<0>();  // drain the trailing dummy loads before the LDS is released
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
@@ -292,15 +473,33 @@ __global__ __launch_bounds__(256) void gemm_fp8_scalar(GemmArgs g) {
   store4<OUT>(g.out, g.ldo, m, n, n + 1, v, g.bias);
 }
 
+static int num_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 template <int BN, int BM, int OUT>
 static hipError_t launch_mfma(const GemmArgs& g, hipStream_t st) {
+  // LDS: ring of 64-byte K steps within 128 KB, plus 32 KB epilogue staging.
+  constexpr int NST = (128 * 1024) / ((BN + BM) * kBK) > 6 ? 6 : (128 * 1024) / ((BN + BM) * kBK);
   const int64_t nt = ((g.N + BN - 1) / BN) * ((g.M + BM - 1) / BM);
-  if (g.K % kBK == 0)
-    hipLaunchKernelGGL((gemm_fp8_mfma<BN, BM, OUT, false>), dim3(static_cast<unsigned>(nt)),
-                       dim3(256), 0, st, g);
+  const int64_t cus = num_cus();
+  // The ring runs NST steps ahead, which may only reach into the next tile:
+  // with fewer K steps per tile than that, give every tile its own workgroup.
+  const int64_t kt = ((g.K + 2 * kBK - 1) / (2 * kBK)) * 2;
+  const unsigned grid = static_cast<unsigned>(nt < cus || kt < NST ? nt : cus);
+  if (g.K % (2 * kBK) == 0)
+    hipLaunchKernelGGL((gemm_fp8_mfma<BN, BM, NST, OUT, false>), dim3(grid), dim3(256), 0, st, g);
   else
-    hipLaunchKernelGGL((gemm_fp8_mfma<BN, BM, OUT, true>), dim3(static_cast<unsigned>(nt)),
-                       dim3(256), 0, st, g);
+    hipLaunchKernelGGL((gemm_fp8_mfma<BN, BM, NST, OUT, true>), dim3(grid), dim3(256), 0, st, g);
   return hipGetLastError();
 }
 
@@ -318,11 +517,11 @@ static hipError_t dispatch(const GemmArgs& g, hipStream_t st) {
                        dim3(256), 0, st, g);
     return hipGetLastError();
   }
-  // Tile choice: the largest tile that still gives at least one full wave of
-  // workgroups over the 256 CUs.
-  auto tiles = [&](int bn, int bm) { return ((g.N + bn - 1) / bn) * ((g.M + bm - 1) / bm); };
-  if (tiles(256, 256) >= 256) return launch_mfma<256, 256, OUT>(g, st);
-  if (tiles(256, 128) >= 256) return launch_mfma<256, 128, OUT>(g, st);
+  // Tile choice: the largest tile that still gives every CU at least one.
+  const int64_t cus = num_cus();
+  auto tiles = [&](int bn, int bm) __attribute__((always_inline)) { return ((g.N + bn - 1) / bn) * ((g.M + bm - 1) / bm); };
+  if (tiles(256, 256) >= cus) return launch_mfma<256, 256, OUT>(g, st);
+  if (tiles(256, 128) >= cus) return launch_mfma<256, 128, OUT>(g, st);
   return launch_mfma<128, 128, OUT>(g, st);
 }
 
