@@ -87,47 +87,37 @@ __device__ __forceinline__ float sat448(float x) {
   return __builtin_fminf(__builtin_fmaxf(x, -kFp8Max), kFp8Max);
 }
 
-// Torch semantics of `t.to(float8_e4m3fn)` for one value, returned as the
-// replacement byte (0x7F|sign) when the value is NaN or beyond 464, else
-// `ok=true` and the caller converts sat448(x) in hardware.
-__device__ __forceinline__ bool e4m3_in_range(float x) {
-  return __builtin_fabsf(x) <= 464.0f;  // false for NaN
-}
-
+// The gfx950 conversion (v_cvt_pk_fp8_f32, no clamp) matches torch's
+// `.to(float8_e4m3fn)` on every input except NaN: it always writes 0xFF,
+// torch writes 0x7F | sign.  (Verified over all 65536 bf16 bit patterns and
+// the over-range / inf / signed-zero / subnormal cases.)
 __device__ __forceinline__ uint32_t e4m3_nan_byte(float x) {
   return (__float_as_uint(x) >> 24 & 0x80u) | 0x7Fu;
 }
 
-// Four values -> four e4m3 bytes packed little-endian, torch `.to(e4m3)`
-// semantics (no prior clamp).
-__device__ __forceinline__ uint32_t e4m3x4_torch(float a, float b, float c, float d) {
-  uint32_t w = cvt_pk_e4m3<false>(sat448(a), sat448(b), 0u);
-  w = cvt_pk_e4m3<true>(sat448(c), sat448(d), w);
-  if (!(e4m3_in_range(a) && e4m3_in_range(b) && e4m3_in_range(c) && e4m3_in_range(d))) {
+__device__ __forceinline__ uint32_t nan_fix4(uint32_t w, float a, float b, float c, float d) {
+  if (__builtin_expect((a != a) | (b != b) | (c != c) | (d != d), 0)) {
     float v[4] = {a, b, c, d};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (!e4m3_in_range(v[i])) {
-        w = (w & ~(0xFFu << (8 * i))) | (e4m3_nan_byte(v[i]) << (8 * i));
-      }
-    }
+    for (int i = 0; i < 4; ++i)
+      if (v[i] != v[i]) w = (w & ~(0xFFu << (8 * i))) | (e4m3_nan_byte(v[i]) << (8 * i));
   }
   return w;
 }
 
-// Four values that went through torch's `.clamp(-448, 448)` first: NaN
-// survives a torch clamp, so only NaN needs the replacement byte.
+// Four values -> four e4m3 bytes packed little-endian, torch `.to(e4m3)`
+// semantics (no prior clamp): |x| > 464, inf and NaN become NaN codes.
+__device__ __forceinline__ uint32_t e4m3x4_torch(float a, float b, float c, float d) {
+  uint32_t w = cvt_pk_e4m3<true>(c, d, cvt_pk_e4m3<false>(a, b, 0u));
+  return nan_fix4(w, a, b, c, d);
+}
+
+// Four values that went through torch's `.clamp(-448, 448)` first (a NaN
+// survives a torch clamp and becomes 0x7F | sign).
 __device__ __forceinline__ uint32_t e4m3x4_clamped(float a, float b, float c, float d) {
   uint32_t w = cvt_pk_e4m3<false>(sat448(a), sat448(b), 0u);
   w = cvt_pk_e4m3<true>(sat448(c), sat448(d), w);
-  if (__builtin_expect((a != a) | (b != b) | (c != c) | (d != d), 0)) {
-    float v[4] = {a, b, c, d};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (v[i] != v[i]) w = (w & ~(0xFFu << (8 * i))) | (e4m3_nan_byte(v[i]) << (8 * i));
-    }
-  }
-  return w;
+  return nan_fix4(w, a, b, c, d);
 }
 
 __device__ __forceinline__ uint32_t e4m3_torch_byte(float x) {

@@ -50,6 +50,33 @@ __device__ __forceinline__ float silu_bf16(float g) {
   return round_bf16(g / (1.0f + expf(-g)));
 }
 
+// Same value in the vector kernel: the divisor 1 + exp(-g) >= 1 is always
+// finite-positive or +inf, so one reciprocal plus a correction step gives the
+// quotient to within an ulp of the IEEE result before the bf16 rounding.
+__device__ __forceinline__ float silu_bf16_fast(float g) {
+  const float d = 1.0f + expf(-g);
+  const float r = __builtin_amdgcn_rcpf(d);
+  const float y = g * r;
+  const float e = __builtin_fmaf(-y, d, g);
+  return round_bf16(__builtin_copysignf(__builtin_fmaf(e, r, y), g));
+}
+
+// Pairs of bf16 roundings with one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ void round_bf16x2(float& a, float& b) {
+  const uint32_t w = pack_bf16x2(a, b);
+  a = __uint_as_float(w << 16);
+  b = __uint_as_float(w & 0xFFFF0000u);
+}
+
+// NaN-propagating max (v_maximum3_f32): torch's amax propagates NaN.
+__device__ __forceinline__ float maxnan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+__device__ __forceinline__ float wave_maxnan(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = maxnan(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
 // One wave per row, NV vectors of 8 elements per lane held in registers.
 template <int MODE, int NV, bool QOUT>
 __global__ __launch_bounds__(256) void row_kernel_vec(RowArgs a) {
@@ -60,30 +87,43 @@ __global__ __launch_bounds__(256) void row_kernel_vec(RowArgs a) {
   float v[NV][8];
 
   const uint16_t* xr = a.x + row * a.ldx;
+  u32x4 xv[NV], uv[NV];
+  // issue every load of the row first (memory-level parallelism)
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int64_t e = (static_cast<int64_t>(j) * 64 + lane) * 8;
     if (e < K) {
-      u32x4 xv = *reinterpret_cast<const u32x4*>(xr + e);
-      unpack8(xv, v[j]);
-      if (MODE == kSilu) {
-        u32x4 uv = *reinterpret_cast<const u32x4*>(xr + K + e);
-        float u[8];
-        unpack8(uv, u);
+      xv[j] = *reinterpret_cast<const u32x4*>(xr + e);
+      if (MODE == kSilu) uv[j] = *reinterpret_cast<const u32x4*>(xr + K + e);
+      if (MODE == kAddRms) uv[j] = *reinterpret_cast<const u32x4*>(a.res + row * a.ldr + e);
+    }
+  }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[j][i] = round_bf16(silu_bf16(v[j][i]) * u[i]);
+  for (int j = 0; j < NV; ++j) {
+    const int64_t e = (static_cast<int64_t>(j) * 64 + lane) * 8;
+    if (e < K) {
+      unpack8(xv[j], v[j]);
+      if (MODE == kSilu) {
+        float u[8];
+        unpack8(uv[j], u);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[j][i] = silu_bf16_fast(v[j][i]) * u[i];
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) round_bf16x2(v[j][i], v[j][i + 1]);
       }
       if (MODE == kAddRms) {
-        uint16_t* rr = a.res + row * a.ldr;
-        u32x4 rv = *reinterpret_cast<const u32x4*>(rr + e);
         float r[8];
-        unpack8(rv, r);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[j][i] = round_bf16(r[i] + v[j][i]);
+        unpack8(uv[j], r);
         u32x4 o;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = pack_bf16x2(v[j][2 * i], v[j][2 * i + 1]);
-        *reinterpret_cast<u32x4*>(rr + e) = o;
+        for (int i = 0; i < 4; ++i) {
+          v[j][2 * i] = r[2 * i] + v[j][2 * i];
+          v[j][2 * i + 1] = r[2 * i + 1] + v[j][2 * i + 1];
+          o[i] = pack_bf16x2(v[j][2 * i], v[j][2 * i + 1]);
+          v[j][2 * i] = __uint_as_float(o[i] << 16);
+          v[j][2 * i + 1] = __uint_as_float(o[i] & 0xFFFF0000u);
+        }
+        *reinterpret_cast<u32x4*>(a.res + row * a.ldr + e) = o;
       }
     } else {
 #pragma unroll
@@ -108,7 +148,9 @@ __global__ __launch_bounds__(256) void row_kernel_vec(RowArgs a) {
         float w[8];
         unpack8(wv, w);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[j][i] = round_bf16((v[j][i] * rstd) * w[i]);
+        for (int i = 0; i < 8; ++i) v[j][i] = (v[j][i] * rstd) * w[i];
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) round_bf16x2(v[j][i], v[j][i + 1]);
       }
     }
   }
@@ -132,27 +174,44 @@ __global__ __launch_bounds__(256) void row_kernel_vec(RowArgs a) {
 #pragma unroll
   for (int j = 0; j < NV; ++j)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[j][i]));
-  amax = __builtin_fmaxf(wave_max(amax), kAmaxFloor);
+    for (int i = 0; i < 8; ++i) amax = maxnan(amax, __builtin_fabsf(v[j][i]));
+  amax = maxnan(wave_maxnan(amax), kAmaxFloor);
   const float scale = amax / kFp8Max;
   if (lane == 0) a.s[row] = scale;
 
   uint8_t* qrow = a.q + row * a.ldq;
-  // scale >= 1e-12/448 is always normal; an infinite scale (inf in the row)
-  // takes the plain division, which yields torch's 0 / NaN pattern.
-  const bool fast = scale < 3.0e38f;
-  const float r = 1.0f / scale;
+  if (amax < 3.0e38f) {
+    // Finite row: |x / scale| <= 448 (within rounding), where the hardware
+    // conversion equals torch's clamp + convert; the quotient is correctly
+    // rounded (Markstein correction with the row's reciprocal).
+    const float r = 1.0f / scale;
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int64_t e = (static_cast<int64_t>(j) * 64 + lane) * 8;
-    if (e < K) {
-      float t[8];
+    for (int j = 0; j < NV; ++j) {
+      const int64_t e = (static_cast<int64_t>(j) * 64 + lane) * 8;
+      if (e < K) {
+        float t[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) t[i] = fast ? div_rn_shared(v[j][i], scale, r) : v[j][i] / scale;
-      u32x2 o;
-      o[0] = e4m3x4_clamped(t[0], t[1], t[2], t[3]);
-      o[1] = e4m3x4_clamped(t[4], t[5], t[6], t[7]);
-      *reinterpret_cast<u32x2*>(qrow + e) = o;
+        for (int i = 0; i < 8; ++i) t[i] = div_rn_shared(v[j][i], scale, r);
+        u32x2 o;
+        o[0] = cvt_pk_e4m3<true>(t[2], t[3], cvt_pk_e4m3<false>(t[0], t[1], 0u));
+        o[1] = cvt_pk_e4m3<true>(t[6], t[7], cvt_pk_e4m3<false>(t[4], t[5], 0u));
+        *reinterpret_cast<u32x2*>(qrow + e) = o;
+      }
+    }
+  } else {
+    // NaN or inf in the row: plain IEEE division and torch's NaN codes.
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int64_t e = (static_cast<int64_t>(j) * 64 + lane) * 8;
+      if (e < K) {
+        float t[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) t[i] = v[j][i] / scale;
+        u32x2 o;
+        o[0] = e4m3x4_clamped(t[0], t[1], t[2], t[3]);
+        o[1] = e4m3x4_clamped(t[4], t[5], t[6], t[7]);
+        *reinterpret_cast<u32x2*>(qrow + e) = o;
+      }
     }
   }
 }
@@ -205,8 +264,8 @@ __global__ __launch_bounds__(256) void row_kernel_generic(RowArgs a) {
     return;
   }
   float amax = 0.0f;
-  for (int64_t e = lane; e < K; e += 64) amax = __builtin_fmaxf(amax, __builtin_fabsf(value(e)));
-  amax = __builtin_fmaxf(wave_max(amax), kAmaxFloor);
+  for (int64_t e = lane; e < K; e += 64) amax = maxnan(amax, __builtin_fabsf(value(e)));
+  amax = maxnan(wave_maxnan(amax), kAmaxFloor);
   const float scale = amax / kFp8Max;
   if (lane == 0) a.s[row] = scale;
   uint8_t* qrow = a.q + row * a.ldq;
