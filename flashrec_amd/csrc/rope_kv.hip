@@ -53,20 +53,26 @@ __device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
   }
 }
 
-// D = 128, Hq % 4 == 0, Hk % 4 == 0, all head rows 16-byte aligned.
+// D = 128, Hq % HPW == 0, Hk % HPW == 0, all head rows 16-byte aligned.
+// One wave per (token, group of HPW heads of one of q / k / v): 16 lanes per
+// head, HPW / 4 heads per lane, 8 contiguous elements (16 bytes) per lane per
+// head.  All of a wave's loads are issued before any arithmetic so each wave
+// keeps HPW / 4 KB in flight.
 // FUSED: norm + rope + KV store; otherwise plain RoPE of q and k in place
 // (python/flashrec/kernel/sglops.py:64-81, apply_rope_inplace).
-template <bool FUSED>
+template <bool FUSED, int HPW>
 __global__ __launch_bounds__(256) void qk_rope_kv_d128(RopeArgs a) {
+  constexpr int R = HPW / 4;  // heads per lane
   const int lane = threadIdx.x & 63;
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  const int qg = a.Hq >> 2, kg = a.Hk >> 2;
+  const int64_t item =
+      static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int qg = a.Hq / HPW, kg = a.Hk / HPW;
   const int per_tok = FUSED ? qg + 2 * kg : qg + kg;
   const int64_t t = item / per_tok;
   if (t >= a.T) return;
   const int g = static_cast<int>(item - t * per_tok);
-  const int hs = lane >> 4;     // head slot inside the group
-  const int j = lane & 15;      // 8-element chunk inside the head
+  const int hs = lane >> 4;  // head slot inside a group of 4
+  const int j = lane & 15;   // 8-element chunk inside the head
   const int e0 = j * 8;
 
   const int64_t slot = FUSED ? a.loc[t] : 0;
@@ -74,49 +80,34 @@ __global__ __launch_bounds__(256) void qk_rope_kv_d128(RopeArgs a) {
 
   if (FUSED && g >= qg + kg) {  // V: straight e4m3 conversion into the slot
     if (!slot_ok) return;
-    const int h = (g - qg - kg) * 4 + hs;
-    u32x4 xv = *reinterpret_cast<const u32x4*>(a.v + t * a.svt + h * a.svh + e0);
-    float x[8];
-    unpack8(xv, x);
-    u32x2 o;
-    o[0] = e4m3x4_torch(x[0], x[1], x[2], x[3]);
-    o[1] = e4m3x4_torch(x[4], x[5], x[6], x[7]);
-    *reinterpret_cast<u32x2*>(a.vc + slot * a.scvp + h * a.scvh + e0) = o;
+    const int h0 = (g - qg - kg) * HPW + hs;
+    u32x4 xv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      xv[r] = *reinterpret_cast<const u32x4*>(a.v + t * a.svt + (h0 + 4 * r) * a.svh + e0);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float x[8];
+      unpack8(xv[r], x);
+      u32x2 o;
+      o[0] = e4m3x4_torch(x[0], x[1], x[2], x[3]);
+      o[1] = e4m3x4_torch(x[4], x[5], x[6], x[7]);
+      *reinterpret_cast<u32x2*>(a.vc + slot * a.scvp + (h0 + 4 * r) * a.scvh + e0) = o;
+    }
     return;
   }
   const bool is_q = g < qg;
-  const int h = (is_q ? g : g - qg) * 4 + hs;
-  const uint16_t* src = is_q ? a.q + t * a.sqt + h * a.sqh : a.k + t * a.skt + h * a.skh;
+  const int h0 = (is_q ? g : g - qg) * HPW + hs;
+  const uint16_t* src = is_q ? a.q + t * a.sqt + h0 * a.sqh : a.k + t * a.skt + h0 * a.skh;
+  const int64_t hstride = is_q ? a.sqh : a.skh;
   const uint16_t* wp = is_q ? a.qw : a.kw;
-
-  u32x4 xv = *reinterpret_cast<const u32x4*>(src + e0);
-  float x[8];
-  unpack8(xv, x);
-  float rstd = 0.0f;
-  float w[8];
-  if (FUSED) {
-    float ss = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) ss += x[i] * x[i];
-    ss = group_sum<16>(ss);
-    rstd = 1.0f / __builtin_sqrtf(ss / 128.0f + a.eps);
-    u32x4 wv = *reinterpret_cast<const u32x4*>(wp + e0);
-    unpack8(wv, w);
-  }
-  float n[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) n[i] = FUSED ? round_bf16((x[i] * rstd) * w[i]) : x[i];
-
-  // partner half: lane j ^ 8 holds elements e0 +- 64
-  float p[8];
-#pragma unroll
-  for (int i = 0; i < 8; i += 2) {
-    uint32_t mine = pack_bf16x2(n[i], n[i + 1]);  // exact: n is bf16 already
-    uint32_t other = static_cast<uint32_t>(__shfl_xor(static_cast<int>(mine), 8, 64));
-    p[i] = __uint_as_float(other << 16);
-    p[i + 1] = __uint_as_float(other & 0xFFFF0000u);
-  }
   const int64_t pos = a.pos[t];
+
+  u32x4 xv[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) xv[r] = *reinterpret_cast<const u32x4*>(src + 4 * r * hstride + e0);
+  u32x4 wv;
+  if (FUSED) wv = *reinterpret_cast<const u32x4*>(wp + e0);
   if (pos < 0 || pos >= a.cs_rows) return;  // no cache row: leave q / slot untouched
   const float* csr = a.cs + pos * 128;
   const int c0 = e0 & 63;
@@ -126,25 +117,56 @@ __global__ __launch_bounds__(256) void qk_rope_kv_d128(RopeArgs a) {
   const float4 sb = *reinterpret_cast<const float4*>(csr + 64 + c0 + 4);
   const float cv[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w};
   const float sv[8] = {sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, sb.z, sb.w};
-  float y[8];
-  if (j < 8) {
+  float w[8];
+  if (FUSED) unpack8(wv, w);
+
 #pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = round_bf16(n[i] * cv[i] - p[i] * sv[i]);
-  } else {
+  for (int r = 0; r < R; ++r) {
+    float x[8];
+    unpack8(xv[r], x);
+    float n[8];
+    if (FUSED) {
+      float ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = round_bf16(n[i] * cv[i] + p[i] * sv[i]);
-  }
-  if (is_q || !FUSED) {
-    u32x4 o;
+      for (int i = 0; i < 8; ++i) ss += x[i] * x[i];
+      ss = group_sum<16>(ss);
+      const float rstd = 1.0f / __builtin_sqrtf(ss / 128.0f + a.eps);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = pack_bf16x2(y[2 * i], y[2 * i + 1]);
-    uint16_t* dst = is_q ? a.q + t * a.sqt + h * a.sqh : const_cast<uint16_t*>(src);
-    *reinterpret_cast<u32x4*>(dst + e0) = o;
-  } else if (slot_ok) {
-    u32x2 o;
-    o[0] = e4m3x4_torch(y[0], y[1], y[2], y[3]);
-    o[1] = e4m3x4_torch(y[4], y[5], y[6], y[7]);
-    *reinterpret_cast<u32x2*>(a.kc + slot * a.sckp + h * a.sckh + e0) = o;
+      for (int i = 0; i < 8; ++i) n[i] = round_bf16((x[i] * rstd) * w[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) n[i] = x[i];
+    }
+    // partner half: lane j ^ 8 holds elements e0 +- 64
+    float p[8];
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      uint32_t mine = pack_bf16x2(n[i], n[i + 1]);  // exact: n is bf16 already
+      uint32_t other = static_cast<uint32_t>(__shfl_xor(static_cast<int>(mine), 8, 64));
+      p[i] = __uint_as_float(other << 16);
+      p[i + 1] = __uint_as_float(other & 0xFFFF0000u);
+    }
+    float y[8];
+    if (j < 8) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) y[i] = round_bf16(n[i] * cv[i] - p[i] * sv[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) y[i] = round_bf16(n[i] * cv[i] + p[i] * sv[i]);
+    }
+    const int h = h0 + 4 * r;
+    if (is_q || !FUSED) {
+      u32x4 o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = pack_bf16x2(y[2 * i], y[2 * i + 1]);
+      uint16_t* dst = is_q ? a.q + t * a.sqt + h * a.sqh : const_cast<uint16_t*>(a.k + t * a.skt + h * a.skh);
+      *reinterpret_cast<u32x4*>(dst + e0) = o;
+    } else if (slot_ok) {
+      u32x2 o;
+      o[0] = e4m3x4_torch(y[0], y[1], y[2], y[3]);
+      o[1] = e4m3x4_torch(y[4], y[5], y[6], y[7]);
+      *reinterpret_cast<u32x2*>(a.kc + slot * a.sckp + h * a.sckh + e0) = o;
+    }
   }
 }
 
@@ -293,10 +315,14 @@ int fr_qk_norm_rope_store_fp8(void* q, int64_t sqt, int64_t sqh, const void* k, 
                     svt % 8 == 0 && svh % 8 == 0 && al(q_weight, 16) && al(k_weight, 16) &&
                     al(cos_sin_cache, 16) && al(k_cache, 8) && al(v_cache, 8) && sckp % 8 == 0 &&
                     sckh % 8 == 0 && scvp % 8 == 0 && scvh % 8 == 0;
-  if (fast) {
+  if (fast && Hq % 8 == 0 && Hk % 8 == 0) {
+    const int64_t items = T * (Hq / 8 + 2 * (Hk / 8));
+    hipLaunchKernelGGL((qk_rope_kv_d128<true, 8>), dim3(static_cast<unsigned>((items + 3) / 4)),
+                       dim3(256), 0, st, a);
+  } else if (fast) {
     const int64_t items = T * (Hq / 4 + 2 * (Hk / 4));
-    hipLaunchKernelGGL(qk_rope_kv_d128<true>, dim3(static_cast<unsigned>((items + 3) / 4)), dim3(256), 0,
-                       st, a);
+    hipLaunchKernelGGL((qk_rope_kv_d128<true, 4>), dim3(static_cast<unsigned>((items + 3) / 4)),
+                       dim3(256), 0, st, a);
   } else {
     const int64_t items = T * (Hq + 2 * Hk);
     hipLaunchKernelGGL(qk_rope_kv_generic<true>, dim3(static_cast<unsigned>((items + 3) / 4)), dim3(256),
@@ -332,7 +358,7 @@ int fr_rope_inplace(void* q, int64_t sqt, int64_t sqh, void* k, int64_t skt, int
                     al(cos_sin_cache, 16);
   if (fast) {
     const int64_t items = T * (Hq / 4 + Hk / 4);
-    hipLaunchKernelGGL(qk_rope_kv_d128<false>, dim3(static_cast<unsigned>((items + 3) / 4)),
+    hipLaunchKernelGGL((qk_rope_kv_d128<false, 4>), dim3(static_cast<unsigned>((items + 3) / 4)),
                        dim3(256), 0, st, a);
   } else {
     const int64_t items = T * (Hq + Hk);

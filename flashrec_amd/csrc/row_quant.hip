@@ -87,13 +87,14 @@ __global__ __launch_bounds__(256) void row_kernel_vec(RowArgs a) {
   float v[NV][8];
 
   const uint16_t* xr = a.x + row * a.ldx;
-  u32x4 xv[NV], uv[NV];
-  // issue every load of the row first (memory-level parallelism)
+  u32x4 xv[NV], uv[NV], wv[NV];
+  // issue every load of the row (and the norm weight) first
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int64_t e = (static_cast<int64_t>(j) * 64 + lane) * 8;
     if (e < K) {
       xv[j] = *reinterpret_cast<const u32x4*>(xr + e);
+      if (MODE == kRms || MODE == kAddRms) wv[j] = *reinterpret_cast<const u32x4*>(a.w + e);
       if (MODE == kSilu) uv[j] = *reinterpret_cast<const u32x4*>(xr + K + e);
       if (MODE == kAddRms) uv[j] = *reinterpret_cast<const u32x4*>(a.res + row * a.ldr + e);
     }
@@ -144,9 +145,8 @@ __global__ __launch_bounds__(256) void row_kernel_vec(RowArgs a) {
     for (int j = 0; j < NV; ++j) {
       const int64_t e = (static_cast<int64_t>(j) * 64 + lane) * 8;
       if (e < K) {
-        u32x4 wv = *reinterpret_cast<const u32x4*>(a.w + e);
         float w[8];
-        unpack8(wv, w);
+        unpack8(wv[j], w);
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[j][i] = (v[j][i] * rstd) * w[i];
 #pragma unroll
