@@ -47,6 +47,32 @@ def _timed(fn, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
+def _graph_timed(fn, reps: int, iters: int = 20) -> float:
+    """Average ms per call of ``fn(i)`` (i cycling over ``reps`` buffers) from
+    one HIP-graph replay of ``iters`` captured calls: the kernels' own time,
+    without the Python launch overhead that dominates calls of a few us."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(reps):
+            fn(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(iters):
+            fn(i % reps)
+    g.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / iters
+
+
 def _copies(nbytes: int) -> int:
     return max(2, math.ceil(MALL_DEFEAT_BYTES / max(1, nbytes)))
 
@@ -78,9 +104,9 @@ def _gemm_case(dev, m, n, k, steps, warmup, seed, rotate=True):
     return ms, flops / (ms * 1e-3) / 1e12
 
 
-def _bw_case(fn_factory, dev, steps, warmup, nbytes):
+def _bw_case(fn_factory, dev, nbytes, reps):
     step, cleanup = fn_factory()
-    ms = _timed(step, steps, warmup)
+    ms = _graph_timed(step, reps)
     cleanup()
     return ms, nbytes / (ms * 1e-3) / 1e9
 
@@ -100,7 +126,24 @@ def _rms_case(dev, m, h, rotate):
 
         return step, lambda: xs.clear()
 
-    return factory, nbytes
+    return factory, nbytes, reps
+
+
+def _quant_case(dev, m, k):
+    from flashrec_amd.kernel.sglops import per_token_quant_fp8
+
+    nbytes = m * k * 2 + m * k + m * 4
+    reps = _copies(nbytes)
+
+    def factory():
+        xs = [torch.randn(m, k, device=dev).to(torch.bfloat16) for _ in range(reps)]
+
+        def step(i):
+            per_token_quant_fp8(xs[i % reps])
+
+        return step, lambda: xs.clear()
+
+    return factory, nbytes, reps
 
 
 def _silu_case(dev, m, d, rotate):
@@ -117,7 +160,7 @@ def _silu_case(dev, m, d, rotate):
 
         return step, lambda: xs.clear()
 
-    return factory, nbytes
+    return factory, nbytes, reps
 
 
 def _rope_case(dev, t, hq, hk, d, slots, rotate):
@@ -151,37 +194,44 @@ def _rope_case(dev, t, hq, hk, d, slots, rotate):
 
         return step, lambda: bufs.clear()
 
-    return factory, nbytes
+    return factory, nbytes, reps
 
 
-def cpu_baseline(m_sample: int = 32, runs: int = 3):
+def cpu_baseline(target_s: float = 3.0, runs: int = 3):
     """The reference's CPU torch path for the headline GEMM (torch._scaled_mm +
-    per-row/per-channel rescale, python/flashrec/kernel/sglops.py:111-139) on
-    ``m_sample`` rows of config 1; TFLOP/s."""
+    per-row/per-channel rescale, python/flashrec/kernel/sglops.py:111-139) on a
+    row sample of config 1 sized to ~``target_s`` seconds per run (at most all
+    4096 rows), median of ``runs``; TFLOP/s."""
     from oracle import inputs, ops
 
     torch.set_num_threads(os.cpu_count() or 1)
     g = torch.Generator().manual_seed(1)
-    x = torch.randn(m_sample, 2048, generator=g).to(torch.bfloat16)
-    qa, sa = ops.per_token_quant_fp8(x)
+    x = torch.randn(4096, 2048, generator=g).to(torch.bfloat16)
+    qa_all, sa_all = ops.per_token_quant_fp8(x)
     qw, sw = ops.quantize_weight_fp8(inputs.config1_weight())
     b = qw.t()
-    ops.fp8_scaled_mm_torch_cpu(qa[:4], b, sa[:4], sw, torch.bfloat16)  # warm-up
+    ops.fp8_scaled_mm_torch_cpu(qa_all[:32], b, sa_all[:32], sw, torch.bfloat16)  # warm-up
+    t0 = time.perf_counter()
+    ops.fp8_scaled_mm_torch_cpu(qa_all[:64], b, sa_all[:64], sw, torch.bfloat16)  # probe
+    probe = (time.perf_counter() - t0) / 64
+    rows = int(min(4096, max(32, 32 * round(target_s / max(probe, 1e-9) / 32))))
+    qa, sa = qa_all[:rows], sa_all[:rows]
     times = []
-    for _ in range(runs):
+    while len(times) < runs or (sum(times) < 10.0 and len(times) < 30):
         t0 = time.perf_counter()
         ops.fp8_scaled_mm_torch_cpu(qa, b, sa, sw, torch.bfloat16)
         times.append(time.perf_counter() - t0)
+    runs = len(times)
     sec = sorted(times)[len(times) // 2]
-    flops = 2.0 * m_sample * 12288 * 2048
+    flops = 2.0 * rows * 12288 * 2048
     return {
         "value": round(flops / sec / 1e12, 6),
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"gate_up W8A8 GEMM, {m_sample} of 4096 rows x N=12288 x K=2048 through "
-                  f"torch._scaled_mm on CPU (reference sglops.py:111-139), median of {runs}; "
-                  f"os.cpu_count()={os.cpu_count()}",
+        "sample": f"gate_up W8A8 GEMM, {rows} of 4096 rows x N=12288 x K=2048 through "
+                  f"torch._scaled_mm on CPU (reference sglops.py:111-139), median of {runs} "
+                  f"runs of {sec:.2f} s; os.cpu_count()={os.cpu_count()}",
         "seconds_per_sample": round(sec, 3),
     }
 
@@ -193,7 +243,18 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="headline GEMM only")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 20 copies of a 256 MiB buffer (rocprof FETCH/WRITE_SIZE scale)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        src = torch.empty(256 * 2**20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read_per_launch": 256 * 2**20,
+                          "copy_bytes_written_per_launch": 256 * 2**20}))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
               "(the FP8 path is single-GPU; see the sharding note in DESIGN.md)", file=sys.stderr)
@@ -206,6 +267,11 @@ def main() -> int:
 
     m, n, k = 4096, 12288, 2048
     ms, tflops = _gemm_case(dev, m, n, k, args.steps, args.warmup, seed=1)
+    traffic = None
+    prof = os.path.join(ROOT, "profiles", "gemm_fp8_config1_traffic.json")
+    if os.path.exists(prof):
+        with open(prof) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
     result = {
         "metric": "FP8 GEMM TFLOPS + quant/KV-write GB/s at 512-4096 beam rows; % of roofline",
         "value": round(tflops, 2),
@@ -223,7 +289,7 @@ def main() -> int:
                    "a": "e4m3 per-token scale", "b": "e4m3 per-channel scale, column-major"},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP8_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP8_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": traffic},
     }
     extra = {}
     if not args.quick:
@@ -241,15 +307,20 @@ def main() -> int:
             extra[name] = {"ms": round(msx, 5), "TFLOP/s": round(tfx, 2),
                            "frac": round(tfx / PEAK_FP8_TFLOPS, 4)}
         cases = {
-            "config0_rms_fp8_M512_cached": _rms_case(dev, 512, 2048, rotate=False),
+            "config0_rms_fp8_M512": _rms_case(dev, 512, 2048, rotate=False),
             "config0_rms_fp8_M4096": _rms_case(dev, 4096, 2048, rotate=True),
             "rms_fp8_M65536": _rms_case(dev, 65536, 2048, rotate=True),
             "config2_silu_fp8": _silu_case(dev, 4096, 6144, rotate=True),
             "config3_qk_rope_kv": _rope_case(dev, 4096, 16, 8, 128, 65536, rotate=True),
             "qk_rope_kv_T32768": _rope_case(dev, 32768, 16, 8, 128, 65536, rotate=True),
+            "per_token_quant_M65536": _quant_case(dev, 65536, 2048),
+            "silu_fp8_M16384": _silu_case(dev, 16384, 6144, rotate=True),
         }
-        for name, (factory, nbytes) in cases.items():
-            msb, gbs = _bw_case(factory, dev, steps, warm, nbytes)
+        result["extra_timing"] = ("GEMMs: HIP events around back-to-back launches; bandwidth kernels: "
+                                  "one HIP-graph replay of 20 launches; inputs rotated over >512 MB "
+                                  "except the 3 MB config-0 case")
+        for name, (factory, nbytes, reps) in cases.items():
+            msb, gbs = _bw_case(factory, dev, nbytes, reps)
             extra[name] = {"ms": round(msb, 5), "GB/s": round(gbs, 1),
                            "frac": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes}
             torch.cuda.empty_cache()
