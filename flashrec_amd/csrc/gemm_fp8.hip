@@ -211,51 +211,52 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     for (int i = 0; i < IA; ++i)
       oa[i] = static_cast<uint32_t>((tm * BM + (i * 4 + wave) * 16 + lrow) * g.lda + lchunk * 16);
   };
-  // Loads of K step `lk` (0..KT-1) of the cur or nxt tile into `slot`.
-  auto issue = [&](int slot, int lk, bool next) __attribute__((always_inline)) {
+  // Load `l` (0..LOADS-1: weight blocks, then activation blocks) of K step
+  // `lk` (0..KT-1) of the cur or nxt tile into `slot`.
+  auto issue_one = [&](int slot, int lk, bool next, int l) __attribute__((always_inline)) {
     uint8_t* sb = smem + slot * STAGE;
     uint8_t* sa = sb + BN * kBK;
     const uint32_t k0 = static_cast<uint32_t>(lk) * kBK;
     const bool kin = !KTAIL || (k0 + lchunk * 16 < static_cast<uint64_t>(g.K));
-#pragma unroll
-    for (int i = 0; i < IB; ++i) {
-      const uint32_t o = next ? ob_nxt[i] : ob_cur[i];
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(sb + (i * 4 + wave) * 1024), 16,
+    if (l < IB) {
+      const uint32_t o = next ? ob_nxt[l] : ob_cur[l];
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(sb + (l * 4 + wave) * 1024), 16,
                                                kin ? o : kOOB, k0, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < IA; ++i) {
+    } else {
+      const int i = l - IB;
       const uint32_t o = next ? oa_nxt[i] : oa_cur[i];
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(sa + (i * 4 + wave) * 1024), 16,
                                                kin ? o : kOOB, k0, 0, 0);
     }
   };
+  auto issue = [&](int slot, int lk, bool next) __attribute__((always_inline)) {
+#pragma unroll
+    for (int l = 0; l < LOADS; ++l) issue_one(slot, lk, next, l);
+  };
 
   // ---- fragments and MFMAs
   const int fr = lane & 31;        // fragment row inside a 32-row block
   const int c0 = (lane >> 5) * 2;  // first 16-byte chunk of this lane's 32 bytes
+  // Fragments as 16-byte halves: read r (0..2*(FN+FM)-1) fills half r%2 of
+  // weight block r/2, then of activation block r/2 - FN.
   struct Frags {
-    v8i b[FN], a[FM];
+    u32x4 b[FN][2], a[FM][2];
   };
-  auto read_frags = [&](Frags& f, int slot) __attribute__((always_inline)) {
+  auto read_one = [&](Frags& f, int slot, int r) __attribute__((always_inline)) {
     const uint8_t* sb = smem + slot * STAGE;
     const uint8_t* sa = sb + BN * kBK;
-#pragma unroll
-    for (int i = 0; i < FN; ++i) {
-      const int r = wn * WN + i * 32 + fr;
-      u32x4 x0 = *reinterpret_cast<const u32x4*>(sb + swz(r, c0));
-      u32x4 x1 = *reinterpret_cast<const u32x4*>(sb + swz(r, c0 + 1));
-      f.b[i] = v8i{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3],
-                   (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+    const int h = r & 1;
+    if (r < 2 * FN) {
+      const int i = r >> 1;
+      f.b[i][h] = *reinterpret_cast<const u32x4*>(sb + swz(wn * WN + i * 32 + fr, c0 + h));
+    } else {
+      const int j = (r >> 1) - FN;
+      f.a[j][h] = *reinterpret_cast<const u32x4*>(sa + swz(wm * WM + j * 32 + fr, c0 + h));
     }
+  };
+  auto read_frags = [&](Frags& f, int slot) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < FM; ++j) {
-      const int r = wm * WM + j * 32 + fr;
-      u32x4 x0 = *reinterpret_cast<const u32x4*>(sa + swz(r, c0));
-      u32x4 x1 = *reinterpret_cast<const u32x4*>(sa + swz(r, c0 + 1));
-      f.a[j] = v8i{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3],
-                   (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
-    }
+    for (int r = 0; r < 2 * (FN + FM); ++r) read_one(f, slot, r);
   };
   v16f acc[FN][FM];
   auto zero_acc = [&]() __attribute__((always_inline)) {
@@ -266,13 +267,10 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
   };
-  auto mfma_rows = [&](const Frags& f, int i0, int i1) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = i0; i < i1; ++i)
-#pragma unroll
-      for (int j = 0; j < FM; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.b[i], f.a[j], acc[i][j], 0,
-                                                                   0, 0, 0, 0, 0);
+  auto mfma_one = [&](const Frags& f, int i, int j) __attribute__((always_inline)) {
+    const v8i bv = (v8i)__builtin_shufflevector(f.b[i][0], f.b[i][1], 0, 1, 2, 3, 4, 5, 6, 7);
+    const v8i av = (v8i)__builtin_shufflevector(f.a[j][0], f.a[j][1], 0, 1, 2, 3, 4, 5, 6, 7);
+    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, acc[i][j], 0, 0, 0, 0, 0, 0);
   };
 
   // ---- epilogue of one tile.  Lane l holds, per block (i, j), output row
@@ -403,12 +401,15 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   read_frags(f0, 0);
 
   // ---- main loop.  Step s (tile s / KT, K step kt = s % KT) holds its
-  // fragments in `cur`: multiply all but the last weight block row; wait for
-  // step s+1 (own loads, then everyone's through the barrier, which also
-  // retires every wave's reads of slot s % NST); refill that slot with step
-  // s+NST; read step s+1's fragments into `nxt` while the last row's MFMAs
-  // run.  Every step has the same shape: past the end the ring loads zeros
-  // and the last fragment read is discarded.
+  // fragments in `cur`.  It first waits for step s+1's slot (own loads, then
+  // everyone's through the barrier, which also retires every wave's reads of
+  // slot s % NST, read into registers during step s-1), refills that slot
+  // with step s+NST, and then runs all of its MFMAs with step s+1's fragment
+  // reads spread over the first three quarters of them and the refill loads
+  // over the last three quarters, so the LDS reads of the CU's four waves
+  // overlap the matrix work instead of stalling the next step.  Every step has the same shape:
+  // past the end the ring loads zeros and the last fragment read is
+  // discarded.
   //
   // vmcnt retires loads in order but counts stores too, so a load wait issued
   // while the epilogue's stores are in flight would also wait for them.
@@ -417,20 +418,36 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   // (whose data needs only those loads) skip the vmcnt wait: the stores get
   // two steps to complete before the next load wait.  Requires NST >= 4.
   static_assert(NST >= 4, "two wait-free steps need a 4-deep ring");
+  constexpr int NMF = FN * FM;                   // MFMAs per step
+  constexpr int NRD = 2 * (FN + FM);             // 16-byte LDS reads per step
+  // Measured on the 4096-row gate_up and down shapes: these placements beat
+  // reads over the first half and loads from the first MFMA or from the half.
+  constexpr int RDU = NMF * 3 / 4;  // MFMAs the fragment reads spread over
+  constexpr int LD0 = NMF / 4;      // first MFMA followed by a ring load
   auto step = [&](Frags& cur, Frags& nxt, int64_t s, int kt, bool wait)
       __attribute__((always_inline)) {
-    mfma_rows(cur, 0, FN - 1);
+    __builtin_amdgcn_sched_barrier(0);
     if (wait) waitcnt_vm<(NST - 2) * LOADS>();
     lds_barrier();
-    const int lk = kt + NST;
-    issue(static_cast<int>(s % NST), lk < KT ? lk : lk - KT, lk >= KT);
-    read_frags(nxt, static_cast<int>((s + 1) % NST));
-    mfma_rows(cur, FN - 1, FN);
-    __builtin_amdgcn_sched_group_barrier(0x020, LOADS, 0);
+    const int lk0 = kt + NST;
+    const int lk = lk0 < KT ? lk0 : lk0 - KT;
+    const bool nx = lk0 >= KT;
+    const int slot = static_cast<int>(s % NST);
+    const int nslot = static_cast<int>((s + 1) % NST);
+    // Unit u: its share of step s+1's fragment reads, MFMA u of step s, its
+    // share of the refill loads.  The sched_barrier keeps units in order, so
+    // the loads leave at the rate the step consumes data and the wave never
+    // stalls on a full load queue while it has MFMAs to issue.
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 2 * (FN + FM) / FM, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    for (int u = 0; u < NMF; ++u) {
+#pragma unroll
+      for (int r = 0; r < NRD; ++r)
+        if (r * RDU / NRD == u) read_one(nxt, nslot, r);
+      mfma_one(cur, u / FM, u % FM);
+#pragma unroll
+      for (int l = 0; l < LOADS; ++l)
+        if (LD0 + l * (NMF - LD0) / LOADS == u) issue_one(slot, lk, nx, l);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
   int64_t s = 0;
