@@ -506,7 +506,10 @@ static int num_cus() {
 template <int BN, int BM, int OUT>
 static hipError_t launch_mfma(const GemmArgs& g, hipStream_t st) {
   // LDS: ring of 64-byte K steps within 128 KB, plus 32 KB epilogue staging.
-  constexpr int NST = (128 * 1024) / ((BN + BM) * kBK) > 6 ? 6 : (128 * 1024) / ((BN + BM) * kBK);
+  // The loads are latency-bound (about 1.3 us from issue to LDS on a busy
+  // chip), so the deepest ring that fits is used: 4, 5 and 8 steps for the
+  // 256x256, 256x128 and 128x128 tiles.
+  constexpr int NST = (128 * 1024) / ((BN + BM) * kBK) > 8 ? 8 : (128 * 1024) / ((BN + BM) * kBK);
   const int64_t nt = ((g.N + BN - 1) / BN) * ((g.M + BM - 1) / BM);
   const int64_t cus = num_cus();
   // The ring runs NST steps ahead, which may only reach into the next tile:
@@ -534,11 +537,13 @@ static hipError_t dispatch(const GemmArgs& g, hipStream_t st) {
                        dim3(256), 0, st, g);
     return hipGetLastError();
   }
-  // Tile choice: the largest tile that still gives every CU at least one.
+  // Tile choice: 256x256 when every CU gets a tile.  Otherwise 256x128 when
+  // that fills at least half the CUs in one round: measured at M=512,
+  // N=12288 (192 tiles), one round of 256x128 beats 1.5 rounds of 128x128.
   const int64_t cus = num_cus();
   auto tiles = [&](int bn, int bm) __attribute__((always_inline)) { return ((g.N + bn - 1) / bn) * ((g.M + bm - 1) / bm); };
   if (tiles(256, 256) >= cus) return launch_mfma<256, 256, OUT>(g, st);
-  if (tiles(256, 128) >= cus) return launch_mfma<256, 128, OUT>(g, st);
+  if (2 * tiles(256, 128) >= cus) return launch_mfma<256, 128, OUT>(g, st);
   return launch_mfma<128, 128, OUT>(g, st);
 }
 
