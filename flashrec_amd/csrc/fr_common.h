@@ -133,12 +133,13 @@ __device__ __forceinline__ uint32_t e4m3_clamped_byte(float x) {
 // correction step: with y faithful and r = RN(1/s), RN(y + r*(x - s*y)) is
 // RN(x/s) barring under/overflow).  The row kernels only call this when s is
 // finite and normal; otherwise they use the plain IEEE division.
-// The quotient takes the sign of x explicitly: for x = -0 the fma chain
-// would produce +0, while IEEE division gives -0 (s > 0 here).
+// The residual is formed as y*s - x and subtracted, so both negations are
+// free source modifiers and a zero quotient keeps the sign of x (-0 / s gives
+// -0, as IEEE division does; s > 0 here): three VALU ops per element.
 __device__ __forceinline__ float div_rn_shared(float x, float s, float r) {
-  float y = x * r;
-  float e = __builtin_fmaf(-y, s, x);
-  return __builtin_copysignf(__builtin_fmaf(e, r, y), x);
+  const float y = x * r;
+  const float e = __builtin_fmaf(y, s, -x);
+  return __builtin_fmaf(-e, r, y);
 }
 
 // ---------------------------------------------------------------- wave64 reductions

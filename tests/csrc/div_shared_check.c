@@ -1,8 +1,9 @@
 /* CPU check of the division the row kernels use for x / scale:
- *   y = x * r;  e = fma(-y, s, x);  q = copysign(fma(e, r, y), x),  r = RN(1/s)
+ *   y = x * r;  e = fma(y, s, -x);  q = fma(-e, r, y),  r = RN(1/s)
  * must equal the IEEE quotient x / s for every x with |x| <= amax,
  * s = RN(amax / 448), whenever the quotient is large enough to change an
- * e4m3 code (|x / s| >= 2^-12; smaller quotients all encode to a signed zero).
+ * e4m3 code (|x / s| >= 2^-12; smaller quotients all encode to a signed zero),
+ * and must carry the quotient's sign always (x = -0 gives -0).
  * x and amax are bf16 values (the rows are bf16 before quantisation).
  * Usage: div_shared_check N SEED -> prints "n=<checked> bad=<mismatches>". */
 #include <math.h>
@@ -27,11 +28,12 @@ int main(int argc, char** argv) {
     float s = a / 448.0f;
     float r = 1.0f / s;
     float y = x * r;
-    float e = fmaf(-y, s, x);
-    float q = copysignf(fmaf(e, r, y), x);
+    float e = fmaf(y, s, -x);
+    float q = fmaf(-e, r, y);
     float t = x / s;
     ++checked;
     if (fabsf(t) >= 0x1p-12f && memcmp(&q, &t, 4) != 0) ++bad;
+    if (signbit(q) != signbit(t)) ++bad;
   }
   printf("n=%ld bad=%ld\n", checked, bad);
   return bad != 0;
