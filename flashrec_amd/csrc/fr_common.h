@@ -161,6 +161,26 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Lane i of each 16-lane row reads lane (i + N) mod 16 of the same row
+// (DPP row_ror:N, a VALU operand modifier, no LDS round trip).  With N = 8
+// this is lane i ^ 8.
+template <int N>
+__device__ __forceinline__ uint32_t row_ror(uint32_t v) {
+  static_assert(N >= 1 && N <= 15, "row_ror range");
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x120 + N, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row_ror8f(float v) { return __uint_as_float(row_ror<8>(__float_as_uint(v))); }
+
+// Sum over each 16-lane row, every lane of the row gets the total.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __uint_as_float(row_ror<8>(__float_as_uint(v)));
+  v += __uint_as_float(row_ror<4>(__float_as_uint(v)));
+  v += __uint_as_float(row_ror<2>(__float_as_uint(v)));
+  v += __uint_as_float(row_ror<1>(__float_as_uint(v)));
+  return v;
+}
+
 // 16-byte vector type for coalesced loads/stores.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));

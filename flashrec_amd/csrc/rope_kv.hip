@@ -116,52 +116,56 @@ __global__ __launch_bounds__(256) void qk_rope_kv_d128(RopeArgs a) {
   const float4 sa = *reinterpret_cast<const float4*>(csr + 64 + c0);
   const float4 sb = *reinterpret_cast<const float4*>(csr + 64 + c0 + 4);
   const float cv[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w};
-  const float sv[8] = {sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, sb.z, sb.w};
+  // rotate-half: the first half subtracts the partner's sin term, the second
+  // adds it; the sign goes into sin once per token (negation is exact)
+  const float sg = j < 8 ? -1.0f : 1.0f;
+  const float sv[8] = {sa.x * sg, sa.y * sg, sa.z * sg, sa.w * sg,
+                       sb.x * sg, sb.y * sg, sb.z * sg, sb.w * sg};
   float w[8];
   if (FUSED) unpack8(wv, w);
 
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    float x[8];
-    unpack8(xv[r], x);
-    float n[8];
+    // the normed head as packed bf16 (the reference rounds it to bf16)
+    u32x4 nb;
     if (FUSED) {
+      float x[8];
+      unpack8(xv[r], x);
       float ss = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ss += x[i] * x[i];
-      ss = group_sum<16>(ss);
-      const float rstd = 1.0f / __builtin_sqrtf(ss / 128.0f + a.eps);
+      for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(x[i], x[i], ss);
+      ss = row16_sum(ss);
+      // mean over D = 128: the power-of-two scale is exact
+      const float rstd = 1.0f / __builtin_sqrtf(ss * (1.0f / 128.0f) + a.eps);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) n[i] = round_bf16((x[i] * rstd) * w[i]);
+      for (int i = 0; i < 4; ++i)
+        nb[i] = pack_bf16x2((x[2 * i] * rstd) * w[2 * i], (x[2 * i + 1] * rstd) * w[2 * i + 1]);
     } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) n[i] = x[i];
+      nb = xv[r];
     }
     // partner half: lane j ^ 8 holds elements e0 +- 64
-    float p[8];
+    float n[8], p[8];
+    unpack8(nb, n);
 #pragma unroll
-    for (int i = 0; i < 8; i += 2) {
-      uint32_t mine = pack_bf16x2(n[i], n[i + 1]);  // exact: n is bf16 already
-      uint32_t other = static_cast<uint32_t>(__shfl_xor(static_cast<int>(mine), 8, 64));
-      p[i] = __uint_as_float(other << 16);
-      p[i + 1] = __uint_as_float(other & 0xFFFF0000u);
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t other = row_ror<8>(nb[i]);
+      p[2 * i] = __uint_as_float(other << 16);
+      p[2 * i + 1] = __uint_as_float(other & 0xFFFF0000u);
     }
-    float y[8];
-    if (j < 8) {
+    // y packed to bf16 once (the reference's bf16 result)
+    u32x4 yb;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) y[i] = round_bf16(n[i] * cv[i] - p[i] * sv[i]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) y[i] = round_bf16(n[i] * cv[i] + p[i] * sv[i]);
-    }
+    for (int i = 0; i < 4; ++i)
+      yb[i] = pack_bf16x2(n[2 * i] * cv[2 * i] + p[2 * i] * sv[2 * i],
+                          n[2 * i + 1] * cv[2 * i + 1] + p[2 * i + 1] * sv[2 * i + 1]);
     const int h = h0 + 4 * r;
     if (is_q || !FUSED) {
-      u32x4 o;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = pack_bf16x2(y[2 * i], y[2 * i + 1]);
+      const u32x4 o = yb;
       uint16_t* dst = is_q ? a.q + t * a.sqt + h * a.sqh : const_cast<uint16_t*>(a.k + t * a.skt + h * a.skh);
       *reinterpret_cast<u32x4*>(dst + e0) = o;
     } else if (slot_ok) {
+      float y[8];
+      unpack8(yb, y);
       u32x2 o;
       o[0] = e4m3x4_torch(y[0], y[1], y[2], y[3]);
       o[1] = e4m3x4_torch(y[4], y[5], y[6], y[7]);
