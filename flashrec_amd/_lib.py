@@ -53,6 +53,11 @@ SIGNATURES = {
     "fr_rope_inplace": [_P, _I64, _I64, _P, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _P],
     "fr_store_kv_fp8": [_P, _I64, _P, _I64, _I32, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _P],
     "fr_log_softmax_f32": [_P, _I64, _P, _I64, _I64, _I64, _P],
+    "fr_paged_attention_fp8": [
+        _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,  # q, k_cache, v_cache + strides
+        _I64, _P, _P, _P,  # num_slots, kv_indices, kv_start, kv_len
+        _P, _I64, _I64, _I64, _I64, _I64, _I64, _F32, _P,  # out + strides, T, Hq, Hk, D, scale, stream
+    ],
 }
 
 _LIB: Optional[ctypes.CDLL] = None

@@ -120,6 +120,24 @@ int fr_store_kv_fp8(const void* k, int64_t skt, const void* v, int64_t svt, int 
                     const int64_t* loc, void* k_cache, int64_t sck, void* v_cache, int64_t scv,
                     int64_t num_slots, int64_t T, int64_t row_dim, void* stream);
 
+/* Paged attention over the e4m3 KV pool, page size 1, head dim 128.
+ * q: [T, Hq, 128] bf16 (token / head strides sqt, sqh in elements);
+ * k_cache, v_cache: [num_slots, Hk, 128] e4m3 (slot / head strides in bytes);
+ * query token t attends to slots kv_indices[kv_start[t] .. + kv_len[t])
+ * (int32; slots outside [0, num_slots) are skipped) with query head h using
+ * kv head h / (Hq / Hk); out: [T, Hq, 128] bf16 = softmax(q k^T * scale) v,
+ * fp32 arithmetic; a token with no visible slot gets zeros.  Decode passes one
+ * token per row (kv_start = kv_indptr[row], kv_len = seq_len); causal
+ * prefill passes, for token j of a row with prefix P, kv_len = P + j + 1.
+ * Replaces the decode / prefill run of python/flashrec/attention/flashinfer.py
+ * :212-238 (AttentionBackend.forward over the plans of :262-378), whose
+ * semantics are those of its _sdpa fallback (:380-431). */
+int fr_paged_attention_fp8(const void* q, int64_t sqt, int64_t sqh, const void* k_cache,
+                           int64_t skp, int64_t skh, const void* v_cache, int64_t svp, int64_t svh,
+                           int64_t num_slots, const int32_t* kv_indices, const int32_t* kv_start,
+                           const int32_t* kv_len, void* out, int64_t sot, int64_t soh, int64_t T,
+                           int64_t Hq, int64_t Hk, int64_t D, float scale, void* stream);
+
 /* Row-wise log_softmax of fp32 logits [M, N] (out may alias x).
  * Replaces the log_softmax of python/flashrec/logits.py:118-120, :136-137. */
 int fr_log_softmax_f32(const float* x, int64_t ldx, float* out, int64_t ldo, int64_t M,

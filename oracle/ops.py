@@ -205,3 +205,61 @@ def restricted_logprobs_fp8(hidden: torch.Tensor, weight: torch.Tensor) -> torch
     qa, sa = per_token_quant_fp8(hidden)
     logits = fp8_scaled_mm(qa, qw.t(), sa, sw)
     return F.log_softmax(logits, dim=-1)
+
+
+# --------------------------------------------------------------- attention
+def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                    kv_indices: torch.Tensor, kv_start: torch.Tensor, kv_len: torch.Tensor,
+                    scale: float) -> torch.Tensor:
+    """python/flashrec/attention/flashinfer.py:380-431 (_sdpa), per query token.
+
+    Token t gathers rows kv_indices[kv_start[t]:kv_start[t]+kv_len[t]] of the
+    e4m3 caches (cast exactly, as ``k_all.to(q.dtype)`` at :386-389 is exact
+    for e4m3), repeats kv heads for grouped queries (:33-37, :406-407) and
+    takes softmax(q k^T * scale) v — here in fp32, rounded to bf16 once (the
+    reference's bf16 SDPA rounds its probabilities to bf16 on the way, so the
+    two differ by bf16 rounding only).  No visible slot: zeros.
+    """
+    T, Hq, D = q.shape
+    Hk = k_cache.shape[1]
+    rep = Hq // Hk
+    out = torch.zeros(T, Hq, D, dtype=torch.float32)
+    kf = k_cache.float()
+    vf = v_cache.float()
+    for t in range(T):
+        n = int(kv_len[t])
+        if n == 0:
+            continue
+        s0 = int(kv_start[t])
+        idx = kv_indices[s0:s0 + n].long()
+        k = kf[idx].repeat_interleave(rep, dim=1)  # [n, Hq, D]
+        v = vf[idx].repeat_interleave(rep, dim=1)
+        qt = q[t].float()  # [Hq, D]
+        sc = torch.einsum("hd,nhd->hn", qt, k) * scale
+        p = torch.softmax(sc, dim=-1)
+        out[t] = torch.einsum("hn,nhd->hd", p, v)
+    return out.to(torch.bfloat16)
+
+
+def sdpa_reference_style(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                         kv_indices: torch.Tensor, kv_indptr: torch.Tensor) -> torch.Tensor:
+    """The decode branch of flashinfer.py:380-431 as its own sequence of torch
+    calls (gather, cast to bf16, NHD -> BHSD permute, repeat_kv,
+    F.scaled_dot_product_attention with scale D^-0.5), one query per row."""
+    rows, Hq, D = q.shape
+    Hk = k_cache.shape[1]
+    rep = Hq // Hk
+    k_all = k_cache.to(q.dtype)
+    v_all = v_cache.to(q.dtype)
+    outs = []
+    for i in range(rows):
+        idx = kv_indices[int(kv_indptr[i]):int(kv_indptr[i + 1])].long()
+        k_t = k_all[idx].permute(1, 0, 2).unsqueeze(0)
+        v_t = v_all[idx].permute(1, 0, 2).unsqueeze(0)
+        q_t = q[i:i + 1].permute(1, 0, 2).unsqueeze(0)
+        b, h, s, d = k_t.shape
+        k_t = k_t[:, :, None].expand(b, h, rep, s, d).reshape(b, h * rep, s, d)
+        v_t = v_t[:, :, None].expand(b, h, rep, s, d).reshape(b, h * rep, s, d)
+        attn = F.scaled_dot_product_attention(q_t, k_t, v_t, scale=D ** -0.5)
+        outs.append(attn.squeeze(0).permute(1, 0, 2))
+    return torch.cat(outs, dim=0)

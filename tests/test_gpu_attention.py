@@ -1,0 +1,211 @@
+"""Parity of the paged fp8 attention kernel (through the C ABI) with the oracle.
+
+Bar: bf16 outputs within 1e-2 of the oracle, max-abs normalised per token and
+head, with the oracle's fp32 softmax(q k^T * scale) v; masked (out-of-pool)
+slots must contribute nothing, a token with no slot gives zeros."""
+
+import pytest
+import torch
+
+from oracle import ops
+
+pytestmark = pytest.mark.gpu
+
+E4M3 = torch.float8_e4m3fn
+SCALE = 128 ** -0.5
+
+
+def _pool(slots, hk, seed, spread=1.0):
+    g = torch.Generator().manual_seed(seed)
+    k = (torch.randn(slots, hk, 128, generator=g) * spread).to(E4M3)
+    v = (torch.randn(slots, hk, 128, generator=g)).to(E4M3)
+    return k, v
+
+
+def _check(got, ref, tol=1e-2):
+    got = got.cpu().float()
+    ref = ref.float()
+    err = (got - ref).abs().amax(-1)
+    mag = ref.abs().amax(-1).clamp(min=1e-6)
+    worst = (err / mag).max().item()
+    assert worst < tol, f"max-abs normalised error {worst:.3e}"
+
+
+def _run(dev, q, k, v, idx, start, ln):
+    from flashrec_amd.attention import paged_attention
+
+    return paged_attention(q.to(dev), k.to(dev), v.to(dev), idx.to(dev), start.to(dev), ln.to(dev), SCALE)
+
+
+@pytest.mark.parametrize("hq,hk", [(16, 8), (8, 8), (16, 4), (16, 2)])
+def test_decode_ragged(dev, hq, hk):
+    """Rows of 1 .. 1000 keys (across and inside the 8 * NP key chunks)."""
+    lens = [1, 2, 7, 8, 9, 63, 64, 65, 128, 130, 257, 1000]
+    slots = 4096
+    k, v = _pool(slots, hk, hq + hk)
+    g = torch.Generator().manual_seed(1)
+    idx = torch.cat([torch.randint(1, slots, (n,), generator=g, dtype=torch.int32) for n in lens])
+    start = torch.zeros(len(lens), dtype=torch.int32)
+    start[1:] = torch.cumsum(torch.tensor(lens[:-1], dtype=torch.int32), 0)
+    ln = torch.tensor(lens, dtype=torch.int32)
+    q = torch.randn(len(lens), hq, 128, generator=g).to(torch.bfloat16)
+    _check(_run(dev, q, k, v, idx, start, ln), ops.paged_attention(q, k, v, idx, start, ln, SCALE))
+
+
+def test_shared_prefix_beams(dev):
+    """Config-4 shape in small: beams of a request share a 128-slot prefix and
+    own a few decode slots each."""
+    beams, prefix, own, hq, hk = 64, 128, 3, 16, 8
+    slots = 2048
+    k, v = _pool(slots, hk, 11, spread=2.0)
+    g = torch.Generator().manual_seed(2)
+    pre = torch.randperm(slots - 1, generator=g)[:prefix].to(torch.int32) + 1
+    rows = [torch.cat([pre, torch.randint(1, slots, (own,), generator=g, dtype=torch.int32)]) for _ in range(beams)]
+    idx = torch.cat(rows)
+    ln = torch.full((beams,), prefix + own, dtype=torch.int32)
+    start = torch.arange(beams, dtype=torch.int32) * (prefix + own)
+    q = (torch.randn(beams, hq, 128, generator=g) * 2).to(torch.bfloat16)
+    _check(_run(dev, q, k, v, idx, start, ln), ops.paged_attention(q, k, v, idx, start, ln, SCALE))
+
+
+def test_out_of_pool_slots_are_skipped_and_empty_rows_are_zero(dev):
+    slots, hk, hq = 256, 2, 4
+    k, v = _pool(slots, hk, 12)
+    idx = torch.tensor([3, 999, 5, -4, 7, 1 << 30, 9], dtype=torch.int32)
+    start = torch.tensor([0, 0, 7, 1], dtype=torch.int32)
+    ln = torch.tensor([7, 0, 0, 1], dtype=torch.int32)  # row 3 sees only the slot 999
+    q = torch.randn(4, hq, 128).to(torch.bfloat16)
+    got = _run(dev, q, k, v, idx, start, ln).cpu()
+    keep = torch.tensor([3, 5, 7, 9], dtype=torch.int32)
+    ref0 = ops.paged_attention(q[:1], k, v, keep, torch.zeros(1, dtype=torch.int32),
+                               torch.tensor([4], dtype=torch.int32), SCALE)
+    _check(got[:1], ref0)
+    assert torch.count_nonzero(got[1:]) == 0
+
+
+def test_strided_queries(dev):
+    """q as a view into a fused qkv output [T, (Hq + 2 Hk) * D]."""
+    t, hq, hk, slots = 33, 16, 8, 1024
+    k, v = _pool(slots, hk, 13)
+    g = torch.Generator().manual_seed(3)
+    qkv = torch.randn(t, (hq + 2 * hk) * 128, generator=g).to(torch.bfloat16)
+    q = qkv[:, : hq * 128].view(t, hq, 128)
+    lens = torch.randint(1, 200, (t,), generator=g, dtype=torch.int32)
+    idx = torch.randint(1, slots, (int(lens.sum()),), generator=g, dtype=torch.int32)
+    start = torch.zeros(t, dtype=torch.int32)
+    start[1:] = torch.cumsum(lens[:-1], 0)
+    from flashrec_amd.attention import paged_attention
+
+    got = paged_attention(qkv.to(dev)[:, : hq * 128].view(t, hq, 128), k.to(dev), v.to(dev), idx.to(dev),
+                          start.to(dev), lens.to(dev), SCALE)
+    _check(got, ops.paged_attention(q, k, v, idx, start, lens, SCALE))
+
+
+class _Batch:
+    """The fields of flashrec.core.ForwardBatch the backend reads."""
+
+    def __init__(self, **kw):
+        self.__dict__.update(kw)
+
+    @property
+    def n_rows(self):
+        return int(self.seq_lens.numel())
+
+
+def test_backend_decode_and_prefill(dev):
+    """AttentionBackend: store K/V through the pool, then attend, for a decode
+    batch and a causal prefill batch with a cached prefix."""
+    from flashrec_amd.attention.flashinfer import AttentionBackend
+    from flashrec_amd.kvcache.pool import TokenToKVPool
+
+    hq, hk, slots = 16, 8, 512
+    pool = TokenToKVPool(1, slots, hk, 128, E4M3, dev)
+    k0, v0 = _pool(slots, hk, 14)
+    pool.k_cache(0).copy_(k0.to(dev))
+    pool.v_cache(0).copy_(v0.to(dev))
+    be = AttentionBackend(pool, hq, hk, 128)
+    g = torch.Generator().manual_seed(4)
+
+    # decode: 3 rows of 40, 1, 77 slots; the last slot of each row is new
+    lens = [40, 1, 77]
+    rows = [torch.randperm(slots - 1, generator=g)[:n].to(torch.int32) + 1 for n in lens]
+    kv = torch.cat(rows)
+    loc = torch.stack([r[-1] for r in rows]).long()
+    q = torch.randn(3, hq, 128, generator=g).to(torch.bfloat16)
+    knew = torch.randn(3, hk, 128, generator=g).to(torch.bfloat16)
+    vnew = torch.randn(3, hk, 128, generator=g).to(torch.bfloat16)
+    seq = torch.tensor(lens, dtype=torch.int32)
+    b = _Batch(is_prefill=False, seq_lens=seq.to(dev), seq_lens_cpu=seq, kv_indices=kv.to(dev), kv_indptr=None,
+               out_cache_loc=loc.to(dev), extend_seq_lens=None, extend_prefix_lens=None)
+    be.prepare(b)
+    got = be.forward(q.to(dev), knew.to(dev), vnew.to(dev), 0, b)
+    kc, vc = k0.clone(), v0.clone()
+    ops.store_kv(kc, vc, loc, knew, vnew)
+    start = torch.tensor([0, 40, 41], dtype=torch.int32)
+    _check(got, ops.paged_attention(q, kc, vc, kv, start, seq, SCALE))
+
+    # prefill: row 0 has 5 cached + 4 new tokens, row 1 has 0 + 6
+    seqp = [9, 6]
+    ext = [4, 6]
+    rows = [torch.randperm(slots - 1, generator=g)[:n].to(torch.int32) + 1 for n in seqp]
+    kv = torch.cat(rows)
+    loc = torch.cat([rows[0][5:], rows[1]]).long()
+    tq = sum(ext)
+    q = torch.randn(tq, hq, 128, generator=g).to(torch.bfloat16)
+    knew = torch.randn(tq, hk, 128, generator=g).to(torch.bfloat16)
+    vnew = torch.randn(tq, hk, 128, generator=g).to(torch.bfloat16)
+    seq = torch.tensor(seqp, dtype=torch.int32)
+    b = _Batch(is_prefill=True, seq_lens=seq.to(dev), seq_lens_cpu=seq, kv_indices=kv.to(dev), kv_indptr=None,
+               out_cache_loc=loc.to(dev), extend_seq_lens=ext, extend_prefix_lens=[5, 0])
+    be.prepare(b)
+    got = be.forward(q.to(dev), knew.to(dev), vnew.to(dev), 0, b)
+    ops.store_kv(kc, vc, loc, knew, vnew)
+    start = torch.tensor([0] * 4 + [9] * 6, dtype=torch.int32)
+    ln = torch.tensor([6, 7, 8, 9, 1, 2, 3, 4, 5, 6], dtype=torch.int32)
+    _check(got, ops.paged_attention(q, kc, vc, kv, start, ln, SCALE))
+
+
+def test_backend_graph_decode_replays(dev):
+    """Graph decode: the plan lives in persistent buffers; replays after a new
+    prepare() see the new lengths (checked on every replay)."""
+    from flashrec_amd.attention.flashinfer import AttentionBackend
+    from flashrec_amd.kvcache.pool import TokenToKVPool
+
+    hq, hk, slots, bs, maxlen = 16, 8, 1024, 8, 64
+    pool = TokenToKVPool(1, slots, hk, 128, E4M3, dev)
+    k0, v0 = _pool(slots, hk, 15)
+    pool.k_cache(0).copy_(k0.to(dev))
+    pool.v_cache(0).copy_(v0.to(dev))
+    be = AttentionBackend(pool, hq, hk, 128)
+    be.init_graph_wrappers([bs], maxlen)
+    be.begin_graph_decode(bs)
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(bs, hq, 128, generator=g).to(torch.bfloat16).to(dev)
+
+    def batch(lens):
+        kv = torch.cat([torch.randint(1, slots, (n,), generator=g, dtype=torch.int32) for n in lens])
+        seq = torch.tensor(lens, dtype=torch.int32)
+        return _Batch(is_prefill=False, seq_lens=seq.to(dev), seq_lens_cpu=seq, kv_indices=kv.to(dev),
+                      kv_indptr=None, out_cache_loc=None, extend_seq_lens=None, extend_prefix_lens=None), kv, seq
+
+    b, kv, seq = batch([5] * bs)
+    be.prepare(b)
+    out = torch.empty(bs, hq, 128, dtype=torch.bfloat16, device=dev)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        out.copy_(be.forward(q, None, None, 0, b, skip_store=True))
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out.copy_(be.forward(q, None, None, 0, b, skip_store=True))
+    for step in range(4):
+        lens = [int(x) for x in torch.randint(1, maxlen + 1, (bs,), generator=g)]
+        b, kv, seq = batch(lens)
+        be.prepare(b)
+        graph.replay()
+        torch.cuda.synchronize()
+        start = torch.zeros(bs, dtype=torch.int32)
+        start[1:] = torch.cumsum(seq[:-1], 0)
+        _check(out, ops.paged_attention(q.cpu(), k0, v0, kv, start, seq, SCALE))
+    be.end_graph_decode()
