@@ -4,19 +4,24 @@
 // Reference: python/flashrec/attention/flashinfer.py:380-431 (_sdpa, the
 // fallback that defines the result: gather k/v rows by slot, cast to the
 // query dtype, scaled_dot_product_attention with scale D^-0.5, grouped-query
-// heads repeated) and :240-378 (paged KV view and the decode / prefill plans:
-// kv_indptr / kv_indices, page size 1, kv heads in NHD layout).  A query token t sees the slots
-// kv_indices[kv_start[t] .. kv_start[t] + kv_len[t]) — one token per row in
-// decode; in causal prefill, token j of a row with prefix P sees P + j + 1.
+// heads repeated) and :240-378 (paged KV view and the decode / prefill
+// plans: kv_indptr / kv_indices, page size 1, kv heads in NHD layout).  A
+// query token t sees the slots kv_indices[kv_start[t] .. + kv_len[t]) — one
+// token per row in decode; in causal prefill, token j of a row with prefix P
+// sees P + j + 1.
 //
-// Layout: one wave per (query token, kv head) computes the NREP query heads
-// that share that kv head.  Lanes form 8 key groups of 8 lanes; a lane holds
-// 16 of the 128 dims, so one key's K (or V) row for the head is one 128-byte
-// gather per group (16 bytes per lane).  Keys go in chunks of 8 * NP: scores
-// of a chunk stay in registers (pass 1, K), then the chunk is folded into a
-// running max / sum / accumulator (pass 2, V) in the exp2 domain (q carries
-// scale * log2(e)).  Partial sums are merged across the 8 key groups once at
-// the end.  Arithmetic in fp32 (e4m3 and bf16 convert exactly), output bf16.
+// Two kernels share the work of one call, each taking whole groups of
+// 32 / NREP consecutive query tokens (32 query rows):
+//  * paged_attn_grouped_d128 (bf16 MFMA) takes the groups whose tokens all
+//    see the same first 32 slots — beams of one request decoding over their
+//    shared prompt, the common case — and multiplies their shared slot
+//    prefix once for all 32 queries;
+//  * paged_attn_tokens_d128 takes every other group and attends token by
+//    token on the VALU (attend_token).
+// Arithmetic in fp32 (e4m3 and bf16 convert exactly; the MFMA path rounds the
+// probabilities to bf16, as the reference's bf16 SDPA does), output bf16.
+#include <type_traits>
+
 #include "fr_common.h"
 
 namespace fr {
@@ -61,14 +66,16 @@ __device__ __forceinline__ void e4m3x16_to_f32(const u32x4& w, float* f) {
   }
 }
 
+// One (query token t, kv head kh) on the whole wave, VALU arithmetic, for
+// the NREP query heads that share kv head kh.  Lanes form 8 key groups of 8
+// lanes; a lane holds 16 of the 128 dims, so one key's K (or V) row for the
+// head is one 128-byte gather per group (16 bytes per lane).  Keys go in
+// chunks of 8 * NP: scores of a chunk stay in registers (pass 1, K), then the
+// chunk is folded into a running max / sum / accumulator (pass 2, V) in the
+// exp2 domain (q carries scale * log2(e)); the 8 key groups' partial sums
+// are merged once at the end.
 template <int NREP, int NP>
-__global__ __launch_bounds__(256) void paged_attn_d128(AttnArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int64_t item =
-      static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t t = item / a.Hk;
-  if (t >= a.T) return;
-  const int kh = static_cast<int>(item - t * a.Hk);
+__device__ __forceinline__ void attend_token(const AttnArgs& a, int64_t t, int kh, int lane) {
   const int kg = lane >> 3;       // key group
   const int d0 = (lane & 7) * 16;  // first of this lane's 16 dims
 
@@ -203,14 +210,350 @@ __global__ __launch_bounds__(256) void paged_attn_d128(AttnArgs a) {
   }
 }
 
+// Whether every token of the group t0 .. t0 + ntok - 1 sees at least 32
+// slots and the same first 32 of them: the grouped kernel takes exactly
+// these groups (its shared prefix then has at least one 32-key block), the
+// per-token kernel all others.  Wave-uniform; both kernels call this.
+template <int TOK>
+__device__ __forceinline__ bool group_shares_block(const AttnArgs& a, int64_t t0, int lane) {
+  const int ntok = static_cast<int>(min<int64_t>(TOK, a.T - t0));
+  int32_t my_start = 0, my_len = 0x7FFFFFFF;
+  if (lane < ntok) {
+    my_start = a.kv_start[t0 + lane];
+    my_len = a.kv_len[t0 + lane];
+  }
+  int32_t lenmin = my_len;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) lenmin = min(lenmin, __shfl_xor(lenmin, o, 64));
+  if (lenmin < 32) return false;
+  // lane p compares position p % 32 of tokens p / 32, p / 32 + 2, ...
+  const int pos = lane & 31;
+  const int32_t s0 = a.kv_indices[__builtin_amdgcn_readlane(my_start, 0) + pos];
+  bool ok = true;
+  for (int tt = 1 + (lane >> 5); tt < ntok; tt += 2)
+    ok = ok && a.kv_indices[__shfl(my_start, tt, 64) + pos] == s0;
+  return __ballot(!ok) == 0;
+}
+
+// ---------------------------------------------------------------------------
+// Grouped kernel (the default): one wave per (group of 32 / NREP consecutive
+// query tokens, kv head), i.e. 32 query rows, on bf16 MFMA.
+//
+// Beams of one request share their prompt's slots, so consecutive decode
+// rows usually attend to a common slot prefix.  The wave finds the longest
+// prefix P shared by every token of its group (one ballot per 64 positions)
+// and runs it in blocks of 32 keys for all 32 queries at once:
+//   S^T[32 keys x 32 queries] = K . Q^T   (8 x mfma_f32_32x32x16_bf16; each
+//       lane gathers 64 bytes of one key row and converts them to bf16 with
+//       one op per two bytes; dims are taken in the order 64h + 8s + t on
+//       both operands, which leaves the dot products unchanged)
+//   online softmax per query: a lane owns one query column and 16 key rows,
+//       so the block max takes one cross-lane step
+//   O^T[128 x 32] += V^T . P^T  (8 MFMAs; V is staged in LDS as bf16
+//       [key][dim] and read back transposed with ds_read_b64_tr_b16; the keys
+//       of each 16-key chunk are taken in the order the score layout holds
+//       them, so P^T feeds the B operand without a lane exchange)
+// The keys past the shared prefix run through the same block with each
+// token's own keys (NREP per token per block) and every query masked to its
+// own token's keys.  A shared 128-slot prefix is thus read and multiplied
+// once for all 32 queries (config-4 decode: 57 us a layer for 4096 beams,
+// against 189 us token by token).
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4_t* lds_s16x4_t;
+
+// e4m3 x 8 (two dwords, little-endian) -> bf16 x 8, exact
+__device__ __forceinline__ bf16x8_t e4m3x8_to_bf16(uint32_t w0, uint32_t w1) {
+  const bf16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false);
+  const bf16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true);
+  const bf16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false);
+  const bf16x2_t d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true);
+  return bf16x8_t{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+constexpr int kVRow = 288;  // LDS bytes per staged V row: 256 + 32 (bank spread)
+
 template <int NREP>
-static hipError_t launch_attn(const AttnArgs& a, hipStream_t st) {
-  const int64_t items = a.T * a.Hk;
-  // keys per chunk 8 * NP: the chunk's scores and K/V loads stay within the
-  // register budget at every group width
+__global__ __launch_bounds__(256) void paged_attn_grouped_d128(AttnArgs a) {
+  constexpr int TOK = 32 / NREP;  // tokens per group
+  __shared__ __attribute__((aligned(16))) uint8_t lds[4 * 32 * kVRow];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+  const int64_t group = item / a.Hk;
+  const int kh = static_cast<int>(item - group * a.Hk);
+  const int64_t t0 = group * TOK;
+  if (t0 >= a.T) return;
+  // groups without a shared 32-slot block go to paged_attn_tokens_d128
+  if (!group_shares_block<TOK>(a, t0, lane)) return;
+  uint8_t* vs = lds + wave * (32 * kVRow);
+  const int n = lane & 31;  // query column (and key row when loading)
+  const int h = lane >> 5;  // half: dims 64h .. 64h + 63
+
+  // this lane's query: token t0 + n / NREP, head kh * NREP + n % NREP
+  const int64_t tq = t0 + n / NREP;
+  const bool qok = tq < a.T;
+  const int32_t qlen = qok ? a.kv_len[tq] : 0;
+  u32x4 qb[8];
+  {
+    const uint16_t* qp = a.q + (qok ? tq : 0) * a.sqt + (kh * NREP + n % NREP) * a.sqh + 64 * h;
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      qb[s] = qok ? *reinterpret_cast<const u32x4*>(qp + 8 * s) : u32x4{0, 0, 0, 0};
+  }
+
+  // ---- shared slot prefix of the group's tokens.  Lanes 0 .. TOK-1 fetch
+  // the tokens' (start, length) in one load; every comparison load of a
+  // 64-position chunk is issued before any is used.
+  const int ntok = static_cast<int>(min<int64_t>(TOK, a.T - t0));
+  int32_t my_start = 0, my_len = 0x7FFFFFFF;
+  if (lane < ntok) {
+    my_start = a.kv_start[t0 + lane];
+    my_len = a.kv_len[t0 + lane];
+  }
+  int32_t lenmin = my_len;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) lenmin = min(lenmin, __shfl_xor(lenmin, o, 64));
+  int32_t starts[TOK];
+#pragma unroll
+  for (int tt = 0; tt < TOK; ++tt) starts[tt] = __builtin_amdgcn_readlane(my_start, tt);
+  const int32_t* i0 = a.kv_indices + starts[0];
+  int32_t P = 0;
+  for (int32_t c = 0; c < lenmin; c += 64) {
+    const int32_t pos = c + lane;
+    const bool in = pos < lenmin;
+    const int32_t s0 = in ? i0[pos] : 0;
+    int32_t sv[TOK];
+#pragma unroll
+    for (int tt = 1; tt < TOK; ++tt) sv[tt] = (in && tt < ntok) ? a.kv_indices[starts[tt] + pos] : s0;
+    bool ok = in;
+#pragma unroll
+    for (int tt = 1; tt < TOK; ++tt) ok = ok && sv[tt] == s0;
+    const uint64_t bad = __ballot(!ok);
+    if (bad) {
+      P = c + __builtin_ctzll(bad);
+      break;
+    }
+    P = c + 64;
+  }
+  P = min(P, lenmin);
+  const int32_t P32 = P & ~31;
+
+  // ---- running softmax state of this lane's query (the two halves hold the
+  // same m; l and O are per half: O^T rows 32mt + 8(v/4) + 4h + v%4)
+  float m = -__builtin_inff(), l = 0.0f;
+  f32x16_t O[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) O[mt][v] = 0.0f;
+
+  // Blocks of 32 key rows.  Block b < nshared: row n is the shared slot
+  // i0[32b + n] for every query; after that, row r holds position
+  // P32 + j * NREP + r % NREP (j = b - nshared) of token t0 + r / NREP and
+  // each query only sees its own token's rows.
+  const int64_t tk = t0 + n / NREP;
+  const bool tk_ok = tk < a.T;
+  const int32_t klen = tk_ok ? a.kv_len[tk] : 0;
+  const int32_t* ik = a.kv_indices + (tk_ok ? a.kv_start[tk] : 0);
+  int32_t rest = klen - P32;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) rest = max(rest, __shfl_xor(rest, o, 64));
+  const int32_t nshared = P32 / 32;
+  const int32_t nblocks = nshared + (rest > 0 ? (rest + NREP - 1) / NREP : 0);
+
+  struct Loaded {
+    u32x4 kw[4], vw[4];
+    bool ok;
+  };
+  // Gathers are unconditional (an invalid row reads slot 0's bytes); scores
+  // of invalid rows are masked below and their V rows zeroed, so nothing
+  // from them (not even a NaN pattern) reaches the sums.
+  auto load = [&](int32_t bi, Loaded& L) __attribute__((always_inline)) {
+    int32_t slot = -1;
+    if (bi < nshared) {
+      slot = i0[32 * bi + n];
+    } else {
+      const int32_t pos = P32 + (bi - nshared) * NREP + n % NREP;
+      slot = (bi < nblocks && pos < klen) ? ik[pos] : -1;
+    }
+    L.ok = slot >= 0 && slot < a.num_slots;
+    const int64_t sl = L.ok ? slot : 0;
+    const uint8_t* kp = a.kc + sl * a.skp + kh * a.skh + 64 * h;
+    const uint8_t* vp = a.vc + sl * a.svp + kh * a.svh + 64 * h;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      L.kw[i] = *reinterpret_cast<const u32x4*>(kp + 16 * i);
+      L.vw[i] = *reinterpret_cast<const u32x4*>(vp + 16 * i);
+    }
+  };
+
+  auto compute = [&](int32_t bi, Loaded& L, auto own_c) __attribute__((always_inline)) {
+    constexpr bool OWN = decltype(own_c)::value;
+    const int32_t pos_base = P32 + (bi - nshared) * NREP;
+    const uint64_t rows_ok = __ballot(L.ok);  // bit r (r < 32): key row r usable
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) L.vw[i][w] = L.ok ? L.vw[i][w] : 0u;
+    // S^T = K . Q^T
+    f32x16_t S;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) S[v] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const bf16x8_t ka = e4m3x8_to_bf16(L.kw[s / 2][(s % 2) * 2], L.kw[s / 2][(s % 2) * 2 + 1]);
+      S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, __builtin_bit_cast(bf16x8_t, qb[s]), S, 0, 0, 0);
+    }
+    // V rows -> LDS as bf16 [key][dim]
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bf16x8_t lo = e4m3x8_to_bf16(L.vw[i][0], L.vw[i][1]);
+      const bf16x8_t hi = e4m3x8_to_bf16(L.vw[i][2], L.vw[i][3]);
+      *reinterpret_cast<bf16x8_t*>(vs + n * kVRow + 128 * h + 32 * i) = lo;
+      *reinterpret_cast<bf16x8_t*>(vs + n * kVRow + 128 * h + 32 * i + 16) = hi;
+    }
+    // scores of this lane's query against key rows r = 8(v/4) + 4h + v%4
+    float x[16];
+    const bool all_rows = static_cast<uint32_t>(rows_ok) == 0xFFFFFFFFu;
+    if (!OWN && all_rows) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) x[v] = S[v] * a.qscale;
+    } else {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = 8 * (v / 4) + 4 * h + (v % 4);
+        bool ok = (rows_ok >> r) & 1;
+        if (OWN) ok = ok && (r / NREP == n / NREP) && (pos_base + r % NREP < qlen);
+        x[v] = ok ? S[v] * a.qscale : -__builtin_inff();
+      }
+    }
+    float mb = x[0];
+#pragma unroll
+    for (int v = 1; v < 16; ++v) mb = __builtin_fmaxf(mb, x[v]);
+    mb = __builtin_fmaxf(mb, __shfl_xor(mb, 32, 64));
+    // Lazy rescale: probabilities are taken against the reference max m and
+    // may reach 2^8; the accumulators are rescaled only when some query's
+    // block max passes m + 8 (wave-uniform, so O is touched rarely).
+    const bool grow = mb > m + 8.0f;
+    if (__ballot(grow)) {
+      const float mn = grow ? mb : m;
+      const float alpha = (m == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
+      m = mn;
+      l *= alpha;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) O[mt][v] *= alpha;
+    }
+    // m stays -inf only while every row this query saw was masked; then
+    // every x is -inf and the probabilities must be 0, not exp2(NaN)
+    const float mref = m == -__builtin_inff() ? 0.0f : m;
+    float pr[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      pr[v] = __builtin_amdgcn_exp2f(x[v] - mref);  // x = -inf gives 0
+      l += pr[v];
+    }
+    bf16x8_t pb[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int t = 0; t < 8; t += 2) {
+        const uint32_t w = pack_bf16x2(pr[8 * c + t], pr[8 * c + t + 1]);
+        pb[c][t] = __builtin_bit_cast(__bf16, static_cast<uint16_t>(w & 0xFFFFu));
+        pb[c][t + 1] = __builtin_bit_cast(__bf16, static_cast<uint16_t>(w >> 16));
+      }
+    // O^T += V^T . P^T; A[dim][k] through the transposing LDS read
+    const int g = lane >> 4, i16 = lane & 15;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int col = 32 * mt + 16 * (g & 1) + 4 * (i16 & 3);
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int r0 = 16 * c + 4 * h + (i16 >> 2);
+        const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t)(vs + r0 * kVRow + 2 * col));
+        const s16x4_t hi =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t)(vs + (r0 + 8) * kVRow + 2 * col));
+        const bf16x8_t av = __builtin_bit_cast(
+            bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        O[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, pb[c], O[mt], 0, 0, 0);
+      }
+    }
+  };
+
+  // two blocks in flight: block b + 1's gathers are issued before block b
+  // is computed
+  Loaded LA, LB;
+  if (nblocks > 0) load(0, LA);
+  int32_t bi = 0;
+  for (; bi + 1 < nshared; bi += 2) {
+    load(bi + 1, LB);
+    compute(bi, LA, std::false_type{});
+    load(bi + 2, LA);
+    compute(bi + 1, LB, std::false_type{});
+  }
+  if (bi < nshared) {
+    load(bi + 1, LB);
+    compute(bi, LA, std::false_type{});
+    LA = LB;
+    ++bi;
+  }
+  for (; bi < nblocks; bi += 2) {
+    load(bi + 1, LB);
+    compute(bi, LA, std::true_type{});
+    if (bi + 1 >= nblocks) break;
+    load(bi + 2, LA);
+    compute(bi + 1, LB, std::true_type{});
+  }
+
+  // ---- normalise and store this lane's query (64 of its 128 dims)
+  const float lt = l + __shfl_xor(l, 32, 64);
+  if (!qok) return;
+  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+  uint16_t* op = a.out + tq * a.sot + (kh * NREP + n % NREP) * a.soh;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      u32x2 w;
+      w[0] = pack_bf16x2(O[mt][4 * j] * inv, O[mt][4 * j + 1] * inv);
+      w[1] = pack_bf16x2(O[mt][4 * j + 2] * inv, O[mt][4 * j + 3] * inv);
+      *reinterpret_cast<u32x2*>(op + 32 * mt + 8 * j + 4 * h) = w;
+    }
+}
+
+// The groups grouped_d128 leaves: one workgroup per group; its waves (8, or
+// 4 for 8-wide query groups, whose per-token registers need a whole SIMD
+// half) take the group's (token, kv head) pairs in turn, each on the VALU.
+template <int NREP>
+constexpr int token_waves() { return NREP >= 8 ? 4 : 8; }
+
+template <int NREP>
+__global__ __launch_bounds__(64 * token_waves<NREP>()) void paged_attn_tokens_d128(AttnArgs a) {
+  constexpr int TOK = 32 / NREP;
   constexpr int NP = NREP >= 8 ? 1 : 16 / NREP;
-  hipLaunchKernelGGL((paged_attn_d128<NREP, NP>), dim3(static_cast<unsigned>((items + 3) / 4)),
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * TOK;
+  if (t0 >= a.T || group_shares_block<TOK>(a, t0, lane)) return;
+  const int ntok = static_cast<int>(min<int64_t>(TOK, a.T - t0));
+  const int pairs = ntok * static_cast<int>(a.Hk);
+  for (int p = wave; p < pairs; p += token_waves<NREP>())
+    attend_token<NREP, NP>(a, t0 + p / a.Hk, static_cast<int>(p % a.Hk), lane);
+}
+
+// Two launches on the stream: every group is taken by exactly one of them.
+template <int NREP>
+static hipError_t launch_grouped(const AttnArgs& a, hipStream_t st) {
+  const int64_t groups = (a.T + 32 / NREP - 1) / (32 / NREP);
+  const int64_t items = groups * a.Hk;
+  hipLaunchKernelGGL((paged_attn_grouped_d128<NREP>), dim3(static_cast<unsigned>((items + 3) / 4)),
                      dim3(256), 0, st, a);
+  hipLaunchKernelGGL((paged_attn_tokens_d128<NREP>), dim3(static_cast<unsigned>(groups)),
+                     dim3(64 * token_waves<NREP>()), 0, st, a);
   return hipGetLastError();
 }
 
@@ -256,10 +599,10 @@ extern "C" int fr_paged_attention_fp8(const void* q, int64_t sqt, int64_t sqh, c
   a.qscale = scale * 1.4426950408889634f;
   hipError_t e;
   switch (Hq / Hk) {
-    case 1: e = launch_attn<1>(a, static_cast<hipStream_t>(stream)); break;
-    case 2: e = launch_attn<2>(a, static_cast<hipStream_t>(stream)); break;
-    case 4: e = launch_attn<4>(a, static_cast<hipStream_t>(stream)); break;
-    case 8: e = launch_attn<8>(a, static_cast<hipStream_t>(stream)); break;
+    case 1: e = launch_grouped<1>(a, static_cast<hipStream_t>(stream)); break;
+    case 2: e = launch_grouped<2>(a, static_cast<hipStream_t>(stream)); break;
+    case 4: e = launch_grouped<4>(a, static_cast<hipStream_t>(stream)); break;
+    case 8: e = launch_grouped<8>(a, static_cast<hipStream_t>(stream)); break;
     default: return FR_EUNSUPPORTED;
   }
   return e == hipSuccess ? FR_OK : FR_ELAUNCH;

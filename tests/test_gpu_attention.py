@@ -209,3 +209,44 @@ def test_backend_graph_decode_replays(dev):
         start[1:] = torch.cumsum(seq[:-1], 0)
         _check(out, ops.paged_attention(q.cpu(), k0, v0, kv, start, seq, SCALE))
     be.end_graph_decode()
+
+
+@pytest.mark.parametrize("hq,hk", [(16, 8), (8, 8), (16, 4), (16, 2)])
+def test_grouped_prefixes_with_ragged_suffixes(dev, hq, hk):
+    """Groups of consecutive tokens share slot prefixes of 33 .. 160 (the
+    MFMA blocks) and own 0 .. 70 further slots each (the masked per-token
+    blocks); one shared slot is outside the pool; T is not a multiple of
+    the group size."""
+    slots = 8192
+    k, v = _pool(slots, hk, 20 + hq + hk, spread=1.5)
+    g = torch.Generator().manual_seed(21)
+    rows, lens = [], []
+    tok = 32 // (hq // hk)
+    for grp, plen in enumerate([33, 64, 100, 160, 47]):
+        pre = torch.randint(1, slots, (plen,), generator=g, dtype=torch.int32)
+        if grp == 2:
+            pre[10] = slots + 5  # outside the pool: skipped for every token of the group
+        ntok = tok if grp < 4 else tok - 3
+        for _ in range(ntok):
+            own = int(torch.randint(0, 71, (1,), generator=g))
+            rows.append(torch.cat([pre, torch.randint(1, slots, (own,), generator=g, dtype=torch.int32)]))
+            lens.append(plen + own)
+    idx = torch.cat(rows)
+    ln = torch.tensor(lens, dtype=torch.int32)
+    start = torch.zeros(len(lens), dtype=torch.int32)
+    start[1:] = torch.cumsum(ln[:-1], 0)
+    q = (torch.randn(len(lens), hq, 128, generator=g) * 2).to(torch.bfloat16)
+    got = _run(dev, q, k, v, idx, start, ln)
+    # the oracle skips nothing: drop the out-of-pool slot from the expectation
+    ref_rows = []
+    keep_idx, keep_start, keep_len = [], [], []
+    off = 0
+    for r in rows:
+        kept = r[(r >= 0) & (r < slots)]
+        keep_idx.append(kept)
+        keep_start.append(off)
+        keep_len.append(int(kept.numel()))
+        off += int(kept.numel())
+    ref = ops.paged_attention(q, k, v, torch.cat(keep_idx), torch.tensor(keep_start, dtype=torch.int32),
+                              torch.tensor(keep_len, dtype=torch.int32), SCALE)
+    _check(got, ref)
