@@ -104,6 +104,54 @@ def _gemm_case(dev, m, n, k, steps, warmup, seed, rotate=True):
     return ms, flops / (ms * 1e-3) / 1e12
 
 
+def _decode_step_case(dev):
+    """Config 4: the 28-layer decode step at 4096 beam rows (8 requests x 512
+    beams over a 128-token shared prompt), one HIP-graph replay per step;
+    its paged attention kernel timed alone over the same batch."""
+    from flashrec_amd.attention import paged_attention
+    from flashrec_amd.decode_step import Qwen3FP8DecodeStep, Qwen3Shape
+
+    shape = Qwen3Shape()
+    m = Qwen3FP8DecodeStep(shape, requests=8, beams=512, prefix=128, step=2, device=dev)
+    m.capture()
+    for _ in range(3):
+        m.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n = 10
+    e0.record()
+    for _ in range(n):
+        m.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / n
+    rows, h, inter = m.rows, shape.hidden, shape.intermediate
+    qkv_n = (shape.q_heads + 2 * shape.kv_heads) * shape.head_dim
+    gemm_flops = shape.layers * 2 * rows * (h * qkv_n + shape.q_heads * shape.head_dim * h
+                                            + h * 2 * inter + inter * h)
+    gemm_flops += 2 * rows * h * shape.sid_tokens
+    out = {"config4_decode_step": {
+        "ms": round(ms, 4), "GEMM_TFLOP/s": round(gemm_flops / (ms * 1e-3) / 1e12, 1),
+        "gemm_tflop_per_step": round(gemm_flops / 1e12, 3), "layers": shape.layers, "rows": rows,
+        "kv_len": m.seq_len, "timing": "one HIP graph per step, mean of 10 replays",
+        "excludes": "trie mask / top-k / beam expand (separate kernel)"}}
+    p = m.attn._plan
+    q = torch.randn(rows, shape.q_heads, shape.head_dim, device=dev).to(torch.bfloat16)
+    o = torch.empty_like(q)
+    k0, v0 = m.pool.k[0], m.pool.v[0]
+
+    def step(_i):
+        paged_attention(q, k0, v0, p["indices"], p["start"], p["len"], shape.head_dim ** -0.5, out=o)
+
+    ms_a = _graph_timed(step, 1)
+    flops = 4.0 * rows * shape.q_heads * m.seq_len * shape.head_dim
+    out["config4_decode_attention"] = {"ms": round(ms_a, 5), "TFLOP/s": round(flops / (ms_a * 1e-3) / 1e12, 1),
+                                       "bound": "bf16 MFMA + gather latency", "rows": rows, "kv_len": m.seq_len}
+    del m
+    torch.cuda.empty_cache()
+    return out
+
+
 def _bw_case(fn_factory, dev, nbytes, reps):
     step, cleanup = fn_factory()
     ms = _graph_timed(step, reps)
@@ -324,6 +372,7 @@ def main() -> int:
             extra[name] = {"ms": round(msb, 5), "GB/s": round(gbs, 1),
                            "frac": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes}
             torch.cuda.empty_cache()
+        extra.update(_decode_step_case(dev))
         result["extra"] = extra
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline()

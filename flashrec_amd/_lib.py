@@ -53,6 +53,15 @@ SIGNATURES = {
     "fr_rope_inplace": [_P, _I64, _I64, _P, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _P],
     "fr_store_kv_fp8": [_P, _I64, _P, _I64, _I32, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _P],
     "fr_log_softmax_f32": [_P, _I64, _P, _I64, _I64, _I64, _P],
+    "fr_genrec_scratch_bytes": [_I64, _I64, _I64],
+    "fr_genrec_mask_topk_expand": [
+        _P, _P, _P, _P, _P, _I64,  # outputs, scratch + bytes
+        _P, _P, _P, _P, _P,  # cum, top_logprobs, top_tokens, node_ids, allow_table
+        _P, _P, _P, _P, _P, _P,  # token_ids in/out, next_node, node_ids_out, do_expand, col
+        _I64, _I64, _I64, _I64,  # token_base, n_nodes, vsz, invalid_node
+        _I64, _I64, _I64, _I64, _I64,  # N, BW, C, K, L
+        _I32, _I32, _I32, _P,  # apply flags, stream
+    ],
     "fr_paged_attention_fp8": [
         _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,  # q, k_cache, v_cache + strides
         _I64, _P, _P, _P,  # num_slots, kv_indices, kv_start, kv_len

@@ -1,0 +1,177 @@
+"""Fused trie mask + top-K + beam expand, interface of ``flashrec.kernel.beam_trie``.
+
+Reference: python/flashrec/kernel/beam_trie.py:229-290 (result tuple,
+workspace), :536-633 (``genrec_mask_topk_expand``).  Backed by the gfx950
+kernels ``fr_genrec_mask_topk_expand`` (flashrec_amd/csrc/beam_trie.hip).
+As in the reference's CUDA path, each beam's candidate row must be sorted
+descending (it comes from a sorted per-row top-k), the expanded token plane
+is written to a workspace ping-pong buffer (never the one it gathers from),
+and ``inplace`` is not honoured (the reference honours it only in its
+PyTorch branch).
+"""
+
+from __future__ import annotations
+
+from typing import Dict, NamedTuple, Optional, Tuple, Union
+
+import torch
+
+from flashrec_amd._lib import call, load, require_device, stream_of
+
+
+class GenrecFusedResult(NamedTuple):
+    vals: torch.Tensor
+    parents: torch.Tensor
+    tokens: torch.Tensor
+    indices: torch.Tensor
+    token_ids: Optional[torch.Tensor]
+    node_ids: Optional[torch.Tensor]
+
+
+class GenrecFusedWorkspace:
+    """Named device buffers reused across steps, grown on demand
+    (beam_trie.py:243-290): ``get`` returns a view of the first ``shape[0]``
+    rows of a buffer whose trailing shape matches."""
+
+    def __init__(self) -> None:
+        self._bufs: Dict[str, torch.Tensor] = {}
+
+    def get(self, name: str, shape: tuple, dtype: torch.dtype, device) -> torch.Tensor:
+        shape = tuple(int(x) for x in shape)
+        device = torch.device(device)
+        if device.type == "cuda" and device.index is None:
+            device = torch.device("cuda", torch.cuda.current_device())
+        t = self._bufs.get(name)
+        fits = (t is not None and t.dtype == dtype and t.device == device and t.ndim == len(shape)
+                and tuple(t.shape[1:]) == shape[1:] and t.shape[0] >= shape[0])
+        if not fits:
+            rows = shape[0]
+            if t is not None and t.dtype == dtype and t.device == device and tuple(t.shape[1:]) == shape[1:]:
+                rows = max(rows, int(t.shape[0]))
+            t = torch.empty((rows,) + shape[1:], dtype=dtype, device=device)
+            self._bufs[name] = t
+        return t[: shape[0]]
+
+    def get_filled(self, name: str, shape: tuple, dtype: torch.dtype, device, value) -> torch.Tensor:
+        before = self._bufs.get(name)
+        view = self.get(name, shape, dtype, device)
+        if before is None or before.data_ptr() != self._bufs[name].data_ptr():
+            self._bufs[name].fill_(value)
+        return view
+
+    def pair(self, name: str, shape: tuple, dtype: torch.dtype, device) -> Tuple[torch.Tensor, torch.Tensor]:
+        return self.get(f"{name}_a", shape, dtype, device), self.get(f"{name}_b", shape, dtype, device)
+
+
+def _same(a: torch.Tensor, b: torch.Tensor) -> bool:
+    return (a.dtype == b.dtype and a.device == b.device and a.shape == b.shape
+            and a.data_ptr() == b.data_ptr() and a.stride() == b.stride())
+
+
+def _pingpong(ws: GenrecFusedWorkspace, name: str, user: torch.Tensor, dtype) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(read, write) planes: the kernel never gathers from the plane it writes
+    (beam_trie.py:371-386)."""
+    a, b = ws.pair(name, tuple(user.shape), dtype, user.device)
+    if _same(user, a):
+        return a, b
+    if _same(user, b):
+        return b, a
+    return user, (b if user.data_ptr() == a.data_ptr() else a)
+
+
+def _i64(t: torch.Tensor) -> torch.Tensor:
+    t = t if t.dtype == torch.int64 else t.to(torch.int64)
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def genrec_mask_topk_expand(
+    cum: torch.Tensor,
+    top_logprobs: torch.Tensor,
+    top_tokens: torch.Tensor,
+    *,
+    select_k: int,
+    node_ids: Optional[torch.Tensor] = None,
+    allow_table: Optional[torch.Tensor] = None,
+    token_base: int = 0,
+    token_ids: Optional[torch.Tensor] = None,
+    col: Union[int, torch.Tensor] = 0,
+    next_node: Optional[torch.Tensor] = None,
+    invalid_node: int = 0,
+    do_expand: Optional[torch.Tensor] = None,
+    apply_mask: bool = True,
+    apply_expand: bool = True,
+    apply_advance: bool = True,
+    inplace: bool = False,
+    workspace: Optional[GenrecFusedWorkspace] = None,
+) -> GenrecFusedResult:
+    """Mask + top-K + expand/advance (beam_trie.py:536-633).
+
+    cum [N, BW] fp32, top_logprobs [N, BW, C] fp32 (rows sorted descending),
+    top_tokens [N, BW, C]; node_ids [N, BW]; allow_table [nodes, vsz]
+    bool/uint8; token_ids [N, BW, L]; next_node [nodes, vsz]; col int or [N].
+    """
+    del inplace
+    require_device(cum, top_logprobs, top_tokens)
+    n, bw = int(cum.shape[0]), int(cum.shape[1])
+    c = int(top_logprobs.shape[2])
+    k = int(select_k)
+    dev = cum.device
+    mask_i = int(bool(apply_mask and node_ids is not None and allow_table is not None))
+    expand_i = int(bool(apply_expand and token_ids is not None))
+    advance_i = int(bool(apply_advance and mask_i and expand_i and next_node is not None))
+    ws = workspace if workspace is not None else GenrecFusedWorkspace()
+    vals = ws.get("vals", (n, k), torch.float32, dev)
+    parents = ws.get("parents", (n, k), torch.int64, dev)
+    tokens = ws.get("sel_tokens", (n, k), torch.int64, dev)
+    indices = ws.get("indices", (n, k), torch.int64, dev)
+    if n == 0:
+        return GenrecFusedResult(vals, parents, tokens, indices, None, None)
+    nbytes = int(load().fr_genrec_scratch_bytes(n, bw, k))
+    if nbytes < 0:
+        raise ValueError(f"select_k={k} outside 1..1024")
+    scratch = ws.get("scratch", (max(nbytes, 8),), torch.uint8, dev)
+    cum_c = cum.to(torch.float32).contiguous()
+    lp_c = top_logprobs.to(torch.float32).contiguous()
+    tok_c = _i64(top_tokens)
+    node_in = allow = None
+    n_nodes = vsz = 0
+    if mask_i:
+        node_in = _i64(node_ids)
+        allow = allow_table.view(torch.uint8) if allow_table.dtype == torch.bool else allow_table
+        if allow.dtype != torch.uint8:
+            raise TypeError(f"allow_table dtype must be bool/uint8, got {allow_table.dtype}")
+        allow = allow.contiguous()
+        n_nodes, vsz = int(allow.shape[0]), int(allow.shape[1])
+    tok_in = tok_out = None
+    width = 0
+    if expand_i:
+        tok_in, tok_out = _pingpong(ws, "tok", _i64(token_ids), torch.int64)
+        width = int(tok_in.shape[-1])
+    col_t = ws.get("col", (n,), torch.int32, dev)
+    if isinstance(col, torch.Tensor):
+        src = col.to(device=dev, dtype=torch.int32).reshape(-1)
+        col_t.copy_(src.expand(n) if src.numel() == 1 else src[:n])
+    else:
+        col_t.fill_(int(col))
+    do_exp = None
+    if do_expand is not None:
+        do_exp = do_expand.to(device=dev, dtype=torch.uint8).reshape(-1).contiguous()
+    nxt = node_out = None
+    if advance_i:
+        nxt = _i64(next_node)
+        node_in, node_out = _pingpong(ws, "node", node_in, torch.int64)
+        if int(nxt.shape[1]) != vsz or int(nxt.shape[0]) != n_nodes:
+            raise ValueError("next_node and allow_table shapes differ")
+
+    def p(t):
+        return 0 if t is None else t.data_ptr()
+
+    call("fr_genrec_mask_topk_expand",
+         vals.data_ptr(), parents.data_ptr(), tokens.data_ptr(), indices.data_ptr(),
+         scratch.data_ptr(), int(scratch.numel()),
+         cum_c.data_ptr(), lp_c.data_ptr(), tok_c.data_ptr(), p(node_in), p(allow),
+         p(tok_in), p(tok_out), p(nxt), p(node_out), p(do_exp), col_t.data_ptr(),
+         int(token_base), n_nodes, vsz, int(invalid_node), n, bw, c, k, width,
+         mask_i, expand_i, advance_i, stream_of(cum))
+    return GenrecFusedResult(vals, parents, tokens, indices,
+                             tok_out if expand_i else None, node_out if advance_i else None)

@@ -138,6 +138,36 @@ int fr_paged_attention_fp8(const void* q, int64_t sqt, int64_t sqh, const void* 
                            const int32_t* kv_len, void* out, int64_t sot, int64_t soh, int64_t T,
                            int64_t Hq, int64_t Hk, int64_t D, float scale, void* stream);
 
+/* Scratch bytes fr_genrec_mask_topk_expand needs for N requests of BW beams
+ * and K picks (-1 when K is outside 1..1024).  No counterpart in the
+ * reference, whose kernel sizes its own scratch (beam_trie.py:462). */
+int fr_genrec_scratch_bytes(int64_t N, int64_t BW, int64_t K);
+
+/* Fused beam step over trie-constrained candidates, per request n < N:
+ * scores = cum[n, b] + top_logprobs[n, b, c] (each beam's C columns sorted
+ * descending, as a sorted per-row top-k gives them), masked by
+ * allow_table[node_ids[n, b]][top_tokens - token_base] when apply_mask
+ * (node < 0 accepts all); top K by score descending then flat index b*C+c
+ * ascending -> out_vals / out_parents (b) / out_tokens / out_indices [N, K];
+ * with apply_expand: token_ids_out[n, b] = token_ids_in[n, parent_b] with
+ * column col[n] set to the picked token (rows b >= K copied); with
+ * apply_advance: node_ids_out[n, b] = next_node[node of parent_b][tok -
+ * token_base] (node < 0 kept, token outside the table -> invalid_node).
+ * Fewer than K valid candidates: the missing picks are (-inf, 0, top_tokens[n,
+ * 0, 0], 0).  token_ids_in and token_ids_out must not alias.  K <= 1024.
+ * Replaces python/flashrec/kernel/beam_trie.py:536-633
+ * (genrec_mask_topk_expand; kernel csrc/beam_trie.cuh:548-757). */
+int fr_genrec_mask_topk_expand(float* out_vals, int64_t* out_parents, int64_t* out_tokens,
+                               int64_t* out_indices, void* scratch, int64_t scratch_bytes,
+                               const float* cum, const float* top_logprobs, const int64_t* top_tokens,
+                               const int64_t* node_ids, const uint8_t* allow_table,
+                               const int64_t* token_ids_in, int64_t* token_ids_out,
+                               const int64_t* next_node, int64_t* node_ids_out,
+                               const uint8_t* do_expand, const int32_t* col, int64_t token_base,
+                               int64_t n_nodes, int64_t vsz, int64_t invalid_node, int64_t N,
+                               int64_t BW, int64_t C, int64_t K, int64_t L, int apply_mask,
+                               int apply_expand, int apply_advance, void* stream);
+
 /* Row-wise log_softmax of fp32 logits [M, N] (out may alias x).
  * Replaces the log_softmax of python/flashrec/logits.py:118-120, :136-137. */
 int fr_log_softmax_f32(const float* x, int64_t ldx, float* out, int64_t ldo, int64_t M,

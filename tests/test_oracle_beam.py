@@ -1,0 +1,98 @@
+"""Pins for oracle/beam.py that do not restate it: torch.topk (an independent
+selection) on tie-free inputs, and small cases whose answers are written out
+by hand."""
+
+import torch
+
+from oracle import beam
+
+NEG = float("-inf")
+
+
+def _sorted_rows(t):
+    return torch.sort(t, dim=-1, descending=True).values
+
+
+def test_matches_torch_topk_without_ties():
+    """The reference's PyTorch branch is a flat torch.topk over the masked
+    scores: with distinct scores and at least K valid candidates the
+    selections agree exactly."""
+    g = torch.Generator().manual_seed(0)
+    n, bw, c, k = 3, 24, 10, 24
+    cum = torch.randn(n, bw, generator=g)
+    lp = _sorted_rows(torch.randn(n, bw, c, generator=g))
+    tok = torch.randint(100, 140, (n, bw, c), generator=g)
+    nodes = torch.randint(-1, 6, (n, bw), generator=g)
+    allow = torch.rand(6, 40, generator=g) > 0.3
+    vals, parents, tokens, idx, _, _ = beam.genrec_mask_topk_expand(cum, lp, tok, k, nodes, allow, 100)
+    scores = (cum[:, :, None] + lp).reshape(n, -1)
+    node = nodes[:, :, None].expand(n, bw, c).reshape(n, -1)
+    rel = tok.reshape(n, -1) - 100
+    ok = allow[node.clamp(min=0), rel] | (node < 0)
+    masked = scores.masked_fill(~ok, NEG)
+    assert ((masked > NEG).sum(1) >= k).all()
+    tv, ti = torch.topk(masked, k, dim=-1, largest=True, sorted=True)
+    assert torch.equal(vals, tv)
+    assert torch.equal(idx, ti)
+    assert torch.equal(parents, ti // c)
+    assert torch.equal(tokens, tok.reshape(n, -1).gather(1, ti))
+
+
+def test_ties_rank_by_flat_index():
+    cum = torch.tensor([[0.0, 0.0, 1.0]])
+    lp = torch.tensor([[[2.0, 1.0], [2.0, 0.5], [1.0, 1.0]]])  # scores 2,1 | 2,0.5 | 2,2
+    tok = torch.arange(6).view(1, 3, 2)
+    vals, parents, tokens, idx, _, _ = beam.genrec_mask_topk_expand(cum, lp, tok, 5)
+    assert idx.tolist() == [[0, 2, 4, 5, 1]]
+    assert vals.tolist() == [[2.0, 2.0, 2.0, 2.0, 1.0]]
+    assert parents.tolist() == [[0, 1, 2, 2, 0]]
+
+
+def test_masked_and_missing_picks():
+    """Node 0 allows only token 11; beam 1 is unconstrained (node -1); the
+    -inf score and the NaN are never picked; 4 picks of 2 valid pad with
+    (-inf, parent 0, index 0, token top_tokens[0, 0, 0])."""
+    cum = torch.tensor([[0.0, 0.0]])
+    lp = torch.tensor([[[3.0, 2.0, 1.0], [float("nan"), 0.5, NEG]]])
+    tok = torch.tensor([[[10, 11, 12], [10, 12, 13]]])
+    nodes = torch.tensor([[0, -1]])
+    allow = torch.zeros(1, 8, dtype=torch.bool)
+    allow[0, 1] = True  # token 11 (base 10)
+    vals, parents, tokens, idx, _, _ = beam.genrec_mask_topk_expand(cum, lp, tok, 4, nodes, allow, 10)
+    assert vals.tolist() == [[2.0, 0.5, NEG, NEG]]
+    assert idx.tolist() == [[1, 4, 0, 0]]
+    assert parents.tolist() == [[0, 1, 0, 0]]
+    assert tokens.tolist() == [[11, 12, 10, 10]]
+
+
+def test_expand_and_advance_by_hand():
+    cum = torch.tensor([[0.0, -1.0, -5.0]])
+    lp = torch.tensor([[[0.0, -2.0], [0.0, -3.0], [0.0, -4.0]]])  # 0,-2 | -1,-4 | -5,-9
+    tok = torch.tensor([[[20, 21], [22, 23], [24, 25]]])
+    nodes = torch.tensor([[1, 2, -1]])
+    allow = torch.ones(3, 8, dtype=torch.bool)
+    nxt = torch.arange(24).view(3, 8)
+    ti = torch.tensor([[[7, 7, 7], [8, 8, 8], [9, 9, 9]]])
+    vals, parents, tokens, idx, tout, nout = beam.genrec_mask_topk_expand(
+        cum, lp, tok, 2, nodes, allow, 20, ti, 1, nxt, -3)
+    assert vals.tolist() == [[0.0, -1.0]]
+    assert parents.tolist() == [[0, 1]]
+    assert tokens.tolist() == [[20, 22]]
+    # rows 0, 1 rebuilt from their parents with column 1 = the new token; row 2 (>= K) copied
+    assert tout.tolist() == [[[7, 20, 7], [8, 22, 8], [9, 9, 9]]]
+    # node of parent 0 is 1 -> next[1][20 - 20] = 8; parent 1 node 2 -> next[2][2] = 18; row 2 copied
+    assert nout.tolist() == [[8, 18, -1]]
+
+
+def test_trie_rules():
+    allow = torch.tensor([[True, False]])
+    nxt = torch.tensor([[5, 6]])
+    assert beam.cand_ok(-1, 999, allow, 10)           # unconstrained
+    assert beam.cand_ok(0, 10, allow, 10)
+    assert not beam.cand_ok(0, 11, allow, 10)
+    assert not beam.cand_ok(0, 12, allow, 10)         # outside the table
+    assert not beam.cand_ok(0, 9, allow, 10)
+    assert beam.transition(-4, 10, nxt, 10, -1) == -4  # unconstrained stays
+    assert beam.transition(0, 11, nxt, 10, -1) == 6
+    assert beam.transition(0, 12, nxt, 10, -1) == -1   # outside -> invalid
+    assert beam.transition(7, 10, nxt, 10, -1) == 5    # node clamped to the table
