@@ -4,9 +4,10 @@ the drop-in operators in the call order of the reference model.
 Reference: python/flashrec/models/qwen3.py:36-136 (attention block), :138-171
 (MLP), :173-223 (decoder layer, fused RMSNorm->fp8 path), :225-320 (model:
 layers, final norm), and python/flashrec/logits.py:118-166 (SID-restricted
-lm_head + log_softmax; fp8 here).  Weights are random (there is no
-checkpoint): bf16 N(0, 0.02) linear weights quantised per output channel with
-the path's own quantiser, norm weights 1 + N(0, 0.1).  The batch is beam
+lm_head + log_softmax; fp8 here).  Weights are either random (bf16 N(0, 0.02)
+linear weights quantised per output channel with the path's own quantiser,
+norm weights 1 + N(0, 0.1)) or loaded from a safetensors checkpoint by
+``flashrec_amd.weight.load_weights``.  The batch is beam
 decode: ``requests`` prompts of ``prefix`` tokens whose KV is written once and
 shared by each request's ``beams`` rows, plus ``step`` decoded tokens per row.
 
@@ -48,6 +49,7 @@ class Qwen3Shape:
     max_position: int = 4096
     sid_tokens: int = 8192
     vocab: int = 151936
+    tie_word_embeddings: bool = True
 
 
 class _Batch:
@@ -62,56 +64,111 @@ class _Batch:
 
 
 class _Layer:
-    def __init__(self, shape: Qwen3Shape, layer_id: int, gen: torch.Generator, device):
+    """One decoder layer's weights, empty until loaded or initialised."""
+
+    def __init__(self, shape: Qwen3Shape, layer_id: int):
         h, d = shape.hidden, shape.head_dim
         nq, nk = shape.q_heads, shape.kv_heads
+        self.layer_id = layer_id
+        self.qkv_proj = Linear(h, (nq + 2 * nk) * d)
+        self.o_proj = Linear(nq * d, h)
+        self.gate_up_proj = Linear(h, 2 * shape.intermediate)
+        self.down_proj = Linear(shape.intermediate, h)
+        self.input_layernorm = RMSNorm(h, shape.eps)
+        self.post_attention_layernorm = RMSNorm(h, shape.eps)
+        self.q_norm = RMSNorm(d, shape.eps)
+        self.k_norm = RMSNorm(d, shape.eps)
 
-        def linear(n_in, n_out):
-            lin = Linear(n_in, n_out)
-            w = (torch.randn(n_out, n_in, generator=gen, device=device) * 0.02).to(torch.bfloat16)
-            lin.load(w, quantize_fp8=True)
-            return lin
+    def linears(self):
+        """(reference module name under ``layers.<i>.``, module)."""
+        return (("self_attn.qkv_proj", self.qkv_proj), ("self_attn.o_proj", self.o_proj),
+                ("mlp.gate_up_proj", self.gate_up_proj), ("mlp.down_proj", self.down_proj))
 
-        def norm(n):
-            rn = RMSNorm(n, shape.eps)
-            rn.weight = torch.nn.Parameter(
+    def norms(self):
+        return (("input_layernorm", self.input_layernorm),
+                ("post_attention_layernorm", self.post_attention_layernorm),
+                ("self_attn.q_norm", self.q_norm), ("self_attn.k_norm", self.k_norm))
+
+
+class Qwen3FP8Weights:
+    """The decoder's parameters under the reference's module names
+    (qwen3.py:225-320): what ``flashrec_amd.weight.load_weights`` fills.
+    Construction allocates nothing on the device."""
+
+    def __init__(self, shape: Qwen3Shape):
+        self.shape = shape
+        self.layers: List[_Layer] = [_Layer(shape, i) for i in range(shape.layers)]
+        self.final_norm = RMSNorm(shape.hidden, shape.eps)
+        self.embed: Optional[torch.Tensor] = None
+        self.lm_head_weight: Optional[torch.Tensor] = None
+        self.tie_word_embeddings = shape.tie_word_embeddings
+
+    def named_linears(self):
+        for L in self.layers:
+            for name, lin in L.linears():
+                yield f"layers.{L.layer_id}.{name}", lin
+
+    def named_norms(self):
+        for L in self.layers:
+            for name, n in L.norms():
+                yield f"layers.{L.layer_id}.{name}", n
+        yield "norm", self.final_norm
+
+    @classmethod
+    def random(cls, shape: Qwen3Shape, gen: torch.Generator, device) -> "Qwen3FP8Weights":
+        """bf16 N(0, 0.02) linear weights quantised per output channel by the
+        path's quantiser; norm weights 1 + N(0, 0.1); tied embedding N(0, 0.02)."""
+        w = cls(shape)
+
+        def norm_weight(n):
+            return torch.nn.Parameter(
                 (1.0 + 0.1 * torch.randn(n, generator=gen, device=device)).to(torch.bfloat16),
                 requires_grad=False)
-            return rn
 
-        self.layer_id = layer_id
-        self.qkv_proj = linear(h, (nq + 2 * nk) * d)
-        self.o_proj = linear(nq * d, h)
-        self.gate_up_proj = linear(h, 2 * shape.intermediate)
-        self.down_proj = linear(shape.intermediate, h)
-        self.input_layernorm = norm(h)
-        self.post_attention_layernorm = norm(h)
-        self.q_norm = norm(d)
-        self.k_norm = norm(d)
+        for L in w.layers:
+            for _, lin in L.linears():
+                lin.load((torch.randn(lin.out_features, lin.in_features, generator=gen, device=device)
+                          * 0.02).to(torch.bfloat16), quantize_fp8=True)
+            for _, n in L.norms():
+                n.weight = norm_weight(n.hidden_size)
+        w.final_norm.weight = norm_weight(shape.hidden)
+        w.embed = (torch.randn(shape.vocab, shape.hidden, generator=gen, device=device) * 0.02
+                   ).to(torch.bfloat16)
+        w.lm_head_weight = w.embed
+        return w
 
 
 class Qwen3FP8DecodeStep:
-    """Random-init Qwen3-shaped decoder plus a decode batch over a shared-prefix KV pool."""
+    """Qwen3-shaped fp8 decoder (random init, or a checkpoint via
+    ``from_pretrained``) plus a synthetic decode batch over a shared-prefix KV pool."""
 
     def __init__(self, shape: Qwen3Shape, requests: int, beams: int, prefix: int, step: int = 1,
-                 device: Optional[torch.device] = None, seed: int = 4):
+                 device: Optional[torch.device] = None, seed: int = 4,
+                 weights: Optional[Qwen3FP8Weights] = None):
         self.shape = shape
         self.device = device or torch.device("cuda")
         dev = self.device
         gen = torch.Generator(device=dev).manual_seed(seed)
-        self.layers: List[_Layer] = [_Layer(shape, i, gen, dev) for i in range(shape.layers)]
-        self.final_norm = RMSNorm(shape.hidden, shape.eps)
-        self.final_norm.weight = torch.nn.Parameter(
-            (1.0 + 0.1 * torch.randn(shape.hidden, generator=gen, device=dev)).to(torch.bfloat16),
-            requires_grad=False)
+        if weights is None:
+            weights = Qwen3FP8Weights.random(shape, gen, dev)
+        for name, lin in weights.named_linears():
+            if not lin._use_fp8:
+                raise ValueError(f"{name} holds no fp8 weight: load with quantize_fp8=True")
+        if weights.lm_head_weight is None:
+            raise ValueError("no lm_head weight (and embeddings are not tied)")
+        self.weights = weights
+        self.layers = weights.layers
+        self.final_norm = weights.final_norm
+        self.embed = weights.lm_head_weight
         self.rotary = RotaryEmbedding(shape.head_dim, shape.max_position, shape.rope_theta, device=dev)
-        # tied embedding [vocab, hidden]; the head reads its SID rows
-        # (logits.py:110-114), here the top of the vocabulary
-        self.embed = (torch.randn(shape.vocab, shape.hidden, generator=gen, device=dev) * 0.02
-                      ).to(torch.bfloat16)
+        # the head reads the SID rows of the lm_head weight (logits.py:110-114),
+        # here the top of the vocabulary
         sid_lo = shape.vocab - shape.sid_tokens
         self.sid_ids = list(range(sid_lo, sid_lo + shape.sid_tokens))
         self.lm_head = RestrictedLMHead(self.sid_ids, fp8=True)
+        # the batch (KV pool contents, hidden states) comes from its own
+        # stream of random numbers, so it is the same for any weights
+        gen = torch.Generator(device=dev).manual_seed(seed + 1000)
 
         # ---- KV pool: each request's prompt KV once, then `step` decoded
         # slots per beam row (slot 0 is the pool's dummy)
@@ -194,6 +251,24 @@ class Qwen3FP8DecodeStep:
         return logprobs
 
     # ---------------------------------------------------------- graph
+    @classmethod
+    def from_pretrained(cls, model_path: str, requests: int, beams: int, prefix: int, step: int = 1,
+                        device: Optional[torch.device] = None, seed: int = 4,
+                        sid_tokens: Optional[int] = None) -> "Qwen3FP8DecodeStep":
+        """Shape from config.json and weights from safetensors (bf16 weights
+        quantised on load, fp8 ones kept with their scales)."""
+        from flashrec_amd.weight import load_hf_config, load_weights
+
+        shape = load_hf_config(model_path)
+        if sid_tokens is not None:
+            shape.sid_tokens = int(sid_tokens)
+        shape.sid_tokens = min(shape.sid_tokens, shape.vocab)
+        shape.max_position = max(shape.max_position, prefix + step + 1)
+        dev = device or torch.device("cuda")
+        w = Qwen3FP8Weights(shape)
+        load_weights(w, model_path, dev, torch.bfloat16, quantize_fp8=True)
+        return cls(shape, requests, beams, prefix, step, dev, seed, weights=w)
+
     def capture(self) -> None:
         """Record forward() into one HIP graph (after a warm-up run that lets
         the lm_head quantise its slice and the allocator settle)."""
