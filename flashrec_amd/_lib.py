@@ -60,8 +60,9 @@ SIGNATURES = {
         _P, _P, _P, _P, _P, _P,  # token_ids in/out, next_node, node_ids_out, do_expand, col
         _I64, _I64, _I64, _I64,  # token_base, n_nodes, vsz, invalid_node
         _I64, _I64, _I64, _I64, _I64,  # N, BW, C, K, L
-        _I32, _I32, _I32, _P,  # apply flags, stream
+        _I32, _I32, _I32, _I32, _P,  # apply flags, next_node is int32, stream
     ],
+    "fr_row_topk": [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P],
     "fr_paged_attention_fp8": [
         _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,  # q, k_cache, v_cache + strides
         _I64, _P, _P, _P,  # num_slots, kv_indices, kv_start, kv_len

@@ -48,7 +48,8 @@ struct GenrecArgs {
   const uint8_t* allow;   // [n_nodes, vsz] or null
   const int64_t* tin;     // [N, BW, L] or null
   int64_t* tout;          // [N, BW, L] or null
-  const int64_t* next;    // [n_nodes, vsz] or null
+  const void* next;       // [n_nodes, vsz] int64 or int32 (next_i32), or null
+  int next_i32;
   int64_t* nout;          // [N, BW] or null
   const uint8_t* do_exp;  // [N] or null (all)
   const int32_t* col;     // [N]
@@ -277,7 +278,9 @@ __global__ __launch_bounds__(1024) void genrec_request_topk_expand(GenrecArgs a)
           nx = a.invalid_node;
         } else {
           const int64_t safe = old > a.n_nodes - 1 ? a.n_nodes - 1 : old;
-          nx = a.next[safe * a.vsz + rel];
+          const int64_t cell = safe * a.vsz + rel;
+          nx = a.next_i32 ? static_cast<int64_t>(static_cast<const int32_t*>(a.next)[cell])
+                          : static_cast<const int64_t*>(a.next)[cell];
         }
       }
       nout[b] = nx;
@@ -301,10 +304,10 @@ extern "C" int fr_genrec_mask_topk_expand(
     float* out_vals, int64_t* out_parents, int64_t* out_tokens, int64_t* out_indices, void* scratch,
     int64_t scratch_bytes, const float* cum, const float* top_logprobs, const int64_t* top_tokens,
     const int64_t* node_ids, const uint8_t* allow_table, const int64_t* token_ids_in,
-    int64_t* token_ids_out, const int64_t* next_node, int64_t* node_ids_out, const uint8_t* do_expand,
+    int64_t* token_ids_out, const void* next_node, int64_t* node_ids_out, const uint8_t* do_expand,
     const int32_t* col, int64_t token_base, int64_t n_nodes, int64_t vsz, int64_t invalid_node,
     int64_t N, int64_t BW, int64_t C, int64_t K, int64_t L, int apply_mask, int apply_expand,
-    int apply_advance, void* stream) {
+    int apply_advance, int next_i32, void* stream) {
   if (N < 0 || BW <= 0 || C <= 0 || K <= 0 || L < 0) return FR_EINVAL;
   if (N == 0) return FR_OK;
   if (!out_vals || !out_parents || !out_tokens || !out_indices || !scratch || !cum || !top_logprobs ||
@@ -330,6 +333,7 @@ extern "C" int fr_genrec_mask_topk_expand(
   a.tin = token_ids_in;
   a.tout = token_ids_out;
   a.next = next_node;
+  a.next_i32 = next_i32 ? 1 : 0;
   a.nout = node_ids_out;
   a.do_exp = do_expand;
   a.col = col;

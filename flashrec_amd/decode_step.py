@@ -144,7 +144,8 @@ class Qwen3FP8DecodeStep:
 
     def __init__(self, shape: Qwen3Shape, requests: int, beams: int, prefix: int, step: int = 1,
                  device: Optional[torch.device] = None, seed: int = 4,
-                 weights: Optional[Qwen3FP8Weights] = None):
+                 weights: Optional[Qwen3FP8Weights] = None, trie_items: int = 0,
+                 trie_levels: int = 3, trie_codes: int = 256):
         self.shape = shape
         self.device = device or torch.device("cuda")
         dev = self.device
@@ -202,7 +203,10 @@ class Qwen3FP8DecodeStep:
         self.attn.prepare(self.batch)
         self.hidden_in = (torch.randn(rows, shape.hidden, generator=gen, device=dev)).to(torch.bfloat16)
         self._graph: Optional[torch.cuda.CUDAGraph] = None
-        self._out: Optional[torch.Tensor] = None
+        self._out = None
+        self.trie = None
+        if trie_items > 0:
+            self._init_beam(requests, beams, trie_items, trie_levels, trie_codes, gen, step)
 
     # ------------------------------------------------------------ one layer
     def _attention(self, L: _Layer, q_fp8, a_scale) -> torch.Tensor:
@@ -251,6 +255,77 @@ class Qwen3FP8DecodeStep:
         return logprobs
 
     # ---------------------------------------------------------- graph
+    # ---------------------------------------------------------- beam tail
+    def _init_beam(self, requests: int, beams: int, items: int, levels: int, codes: int,
+                   gen: torch.Generator, step: int) -> None:
+        """A random trie of ``items`` SIDs of ``levels`` codes each (level l's
+        code c is token sid_lo + l*codes + c) as the dense allow / next tables
+        of python/flashrec/search/trie.py:208-251 (next_node int32, leaves ->
+        -1 = unconstrained, missing children -> the invalid row), and beam
+        state one level deep: each beam has taken a random valid first code."""
+        dev = self.device
+        vsz = levels * codes
+        if vsz > self.shape.sid_tokens:
+            raise ValueError("trie codes exceed the SID head")
+        sids = torch.randint(0, codes, (items, levels), generator=gen, device=dev)
+        # node ids: root 0, then the distinct prefixes of each depth in order
+        node_of = [torch.zeros(items, dtype=torch.int64, device=dev)]
+        n_nodes = 1
+        key = torch.zeros(items, dtype=torch.int64, device=dev)
+        for d in range(1, levels):
+            key = key * codes + sids[:, d - 1]
+            uniq, inv = torch.unique(key, return_inverse=True)
+            node_of.append(n_nodes + inv)
+            n_nodes += int(uniq.numel())
+        invalid = n_nodes
+        allow = torch.zeros(n_nodes + 1, vsz, dtype=torch.bool, device=dev)
+        nxt = torch.full((n_nodes + 1, vsz), invalid, dtype=torch.int32, device=dev)
+        for d in range(levels):
+            rel = d * codes + sids[:, d]
+            allow[node_of[d], rel] = True
+            child = node_of[d + 1].to(torch.int32) if d + 1 < levels else torch.full_like(rel, -1, dtype=torch.int32)
+            nxt[node_of[d], rel] = child
+        n, bw = requests, beams
+        first = sids[torch.randint(0, items, (n, bw), generator=gen, device=dev), 0]
+        self.trie = dict(allow=allow, next=nxt, invalid=invalid, base=self.sid_ids[0], levels=levels,
+                         codes=codes, n_nodes=n_nodes)
+        self.beam_n, self.beam_bw = n, bw
+        self.beam_cand = min(2 * bw, self.shape.sid_tokens)  # beam_candidates (core.py:76-78)
+        self.cand_ids = torch.tensor(self.sid_ids, dtype=torch.int64, device=dev)
+        self.beam_cum = torch.sort(torch.randn(n, bw, generator=gen, device=dev) - 3.0, dim=-1,
+                                   descending=True).values
+        self.beam_nodes = nxt[0, first].to(torch.int64)
+        width = max(levels, step + 1)
+        self.beam_tokens = torch.zeros(n, bw, width, dtype=torch.int64, device=dev)
+        self.beam_tokens[:, :, 0] = self.sid_ids[0] + first
+        self.beam_col = torch.ones(n, dtype=torch.int32, device=dev)
+        from flashrec_amd.kernel.beam_trie import GenrecFusedWorkspace
+
+        self.beam_ws = GenrecFusedWorkspace()
+        self._topk_vals = torch.empty(n, bw, self.beam_cand, dtype=torch.float32, device=dev)
+        self._topk_tok = torch.empty(n, bw, self.beam_cand, dtype=torch.int64, device=dev)
+
+    def beam_step(self, logprobs: torch.Tensor):
+        """The step's tail (scheduler.py:1469-1561): per-row top-C of the SID
+        log-probs with the candidate-id gather, then the fused trie mask +
+        top-K + token-row expand + node advance for every request."""
+        from flashrec_amd.kernel.beam_trie import genrec_mask_topk_expand, row_topk
+
+        if self.trie is None:
+            raise RuntimeError("built without a trie (trie_items=0)")
+        n, bw, c = self.beam_n, self.beam_bw, self.beam_cand
+        vals, _, toks = row_topk(logprobs.view(n, bw, -1), c, self.cand_ids,
+                                 out=(self._topk_vals, None), out_tokens=self._topk_tok, need_idx=False)
+        tr = self.trie
+        return genrec_mask_topk_expand(
+            self.beam_cum, vals, toks, select_k=bw, node_ids=self.beam_nodes, allow_table=tr["allow"],
+            token_base=tr["base"], token_ids=self.beam_tokens, col=self.beam_col, next_node=tr["next"],
+            invalid_node=tr["invalid"], workspace=self.beam_ws)
+
+    def forward_beam(self):
+        """forward() then beam_step(): one whole decode step of beam search."""
+        return self.beam_step(self.forward())
+
     @classmethod
     def from_pretrained(cls, model_path: str, requests: int, beams: int, prefix: int, step: int = 1,
                         device: Optional[torch.device] = None, seed: int = 4,
@@ -269,21 +344,23 @@ class Qwen3FP8DecodeStep:
         load_weights(w, model_path, dev, torch.bfloat16, quantize_fp8=True)
         return cls(shape, requests, beams, prefix, step, dev, seed, weights=w)
 
-    def capture(self) -> None:
-        """Record forward() into one HIP graph (after a warm-up run that lets
-        the lm_head quantise its slice and the allocator settle)."""
+    def capture(self, beam: bool = False) -> None:
+        """Record forward() (with ``beam``, forward_beam()) into one HIP graph
+        after a warm-up run that lets the lm_head quantise its slice and the
+        allocator and workspaces settle."""
+        fn = self.forward_beam if beam else self.forward
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
-            self.forward()
+            fn()
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            self._out = self.forward()
+            self._out = fn()
         self._graph = g
 
-    def replay(self) -> torch.Tensor:
+    def replay(self):
         assert self._graph is not None and self._out is not None
         self._graph.replay()
         return self._out

@@ -157,8 +157,14 @@ def genrec_mask_topk_expand(
     if do_expand is not None:
         do_exp = do_expand.to(device=dev, dtype=torch.uint8).reshape(-1).contiguous()
     nxt = node_out = None
+    next_i32 = 0
     if advance_i:
-        nxt = _i64(next_node)
+        # the trie keeps next_node as int32 (trie.py:220): read it as is
+        # rather than widening the whole table every step
+        if next_node.dtype == torch.int32:
+            nxt, next_i32 = next_node.contiguous(), 1
+        else:
+            nxt = _i64(next_node)
         node_in, node_out = _pingpong(ws, "node", node_in, torch.int64)
         if int(nxt.shape[1]) != vsz or int(nxt.shape[0]) != n_nodes:
             raise ValueError("next_node and allow_table shapes differ")
@@ -172,6 +178,57 @@ def genrec_mask_topk_expand(
          cum_c.data_ptr(), lp_c.data_ptr(), tok_c.data_ptr(), p(node_in), p(allow),
          p(tok_in), p(tok_out), p(nxt), p(node_out), p(do_exp), col_t.data_ptr(),
          int(token_base), n_nodes, vsz, int(invalid_node), n, bw, c, k, width,
-         mask_i, expand_i, advance_i, stream_of(cum))
+         mask_i, expand_i, advance_i, next_i32, stream_of(cum))
     return GenrecFusedResult(vals, parents, tokens, indices,
                              tok_out if expand_i else None, node_out if advance_i else None)
+
+
+def row_topk(
+    scores: torch.Tensor,
+    k: int,
+    cand_ids: Optional[torch.Tensor] = None,
+    *,
+    out: Optional[Tuple[torch.Tensor, Optional[torch.Tensor]]] = None,
+    out_tokens: Optional[torch.Tensor] = None,
+    need_idx: bool = True,
+) -> Tuple[torch.Tensor, Optional[torch.Tensor], torch.Tensor]:
+    """Sorted top-``k`` over the last dim of fp32 ``scores`` [..., V] and the
+    candidate-id gather: (vals, idx, tokens) with tokens = cand_ids[idx] (idx
+    when cand_ids is None).  Stands for ``torch.topk(..., sorted=True)`` +
+    ``fill_topk_tokens`` (scheduler.py:1476-1481, graph.py:33-43, :186-193);
+    equal scores come out by ascending index, NaN first.  ``out`` / ``out_tokens``
+    are caller-owned buffers (graph-capture safe), as in graph.py:186-193.
+    With ``need_idx=False`` the column indices are not written and idx is
+    None (the beam step consumes only scores and tokens).
+    k <= min(V, 1024), V <= 16384."""
+    require_device(scores)
+    if scores.dtype != torch.float32:
+        raise TypeError(f"row_topk takes fp32 scores, got {scores.dtype}")
+    v = int(scores.shape[-1])
+    x = scores.reshape(-1, v)
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    r = int(x.shape[0])
+    shape = tuple(scores.shape[:-1]) + (int(k),)
+    if out is not None:
+        vals, idx = out
+    else:
+        vals = torch.empty(shape, dtype=torch.float32, device=scores.device)
+        idx = torch.empty(shape, dtype=torch.int64, device=scores.device) if need_idx else None
+    if not need_idx:
+        idx = None
+    tokens = out_tokens if out_tokens is not None else torch.empty(shape, dtype=torch.int64,
+                                                                   device=scores.device)
+    for t, dt in ((vals, torch.float32), (idx, torch.int64), (tokens, torch.int64)):
+        if t is not None and (t.dtype != dt or not t.is_contiguous() or t.numel() != r * int(k)):
+            raise ValueError("row_topk output buffers must be contiguous [..., k] fp32/int64")
+    cid = None
+    if cand_ids is not None:
+        cid = _i64(cand_ids.reshape(-1))
+        if int(cid.numel()) < v:
+            raise ValueError(f"cand_ids has {cid.numel()} entries for {v} columns")
+    call("fr_row_topk", x.data_ptr(), x.stride(0) if r > 1 else v, r, v, int(k),
+         0 if cid is None else cid.data_ptr(), vals.data_ptr(), 0 if idx is None else idx.data_ptr(),
+         tokens.data_ptr(),
+         stream_of(scores))
+    return vals, idx, tokens

@@ -152,7 +152,9 @@ int fr_genrec_scratch_bytes(int64_t N, int64_t BW, int64_t K);
  * with apply_expand: token_ids_out[n, b] = token_ids_in[n, parent_b] with
  * column col[n] set to the picked token (rows b >= K copied); with
  * apply_advance: node_ids_out[n, b] = next_node[node of parent_b][tok -
- * token_base] (node < 0 kept, token outside the table -> invalid_node).
+ * token_base] (node < 0 kept, token outside the table -> invalid_node);
+ * next_node is int32 when next_i32 (the trie's own table dtype,
+ * python/flashrec/search/trie.py:220), else int64.
  * Fewer than K valid candidates: the missing picks are (-inf, 0, top_tokens[n,
  * 0, 0], 0).  token_ids_in and token_ids_out must not alias.  K <= 1024.
  * Replaces python/flashrec/kernel/beam_trie.py:536-633
@@ -162,11 +164,23 @@ int fr_genrec_mask_topk_expand(float* out_vals, int64_t* out_parents, int64_t* o
                                const float* cum, const float* top_logprobs, const int64_t* top_tokens,
                                const int64_t* node_ids, const uint8_t* allow_table,
                                const int64_t* token_ids_in, int64_t* token_ids_out,
-                               const int64_t* next_node, int64_t* node_ids_out,
+                               const void* next_node, int64_t* node_ids_out,
                                const uint8_t* do_expand, const int32_t* col, int64_t token_base,
                                int64_t n_nodes, int64_t vsz, int64_t invalid_node, int64_t N,
                                int64_t BW, int64_t C, int64_t K, int64_t L, int apply_mask,
-                               int apply_expand, int apply_advance, void* stream);
+                               int apply_expand, int apply_advance, int next_i32, void* stream);
+
+/* Per-row top-C of fp32 scores x [R, V] (row stride ldx): out_vals [R, C]
+ * sorted descending (NaN above +inf, equal scores by ascending index),
+ * out_idx [R, C] int64 column indices (may be null), out_tokens [R, C] int64
+ * = cand_ids[idx] (or idx when cand_ids is null; out_tokens may be null).
+ * C <= min(V, 1024), V <= 16384.  Replaces the sorted torch.topk over the
+ * stacked beam log-probs and the candidate-id gather that feed the fused beam
+ * step (python/flashrec/scheduler/scheduler.py:1476-1481,
+ * python/flashrec/engine/graph.py:33-43, :186-193). */
+int fr_row_topk(const float* x, int64_t ldx, int64_t R, int64_t V, int64_t C,
+                const int64_t* cand_ids, float* out_vals, int64_t* out_idx, int64_t* out_tokens,
+                void* stream);
 
 /* Row-wise log_softmax of fp32 logits [M, N] (out may alias x).
  * Replaces the log_softmax of python/flashrec/logits.py:118-120, :136-137. */

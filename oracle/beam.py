@@ -1,5 +1,5 @@
-"""Torch-CPU restatement of the fused beam step (trie mask -> top-K -> expand
--> advance).  TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
+"""Torch-CPU restatement of the beam step: the per-row candidate top-k, then
+the fused trie mask -> top-K -> expand -> advance.  TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
 
 python/flashrec/kernel/beam_trie.py:585-633 (the PyTorch branch, the source
 of correctness) fixes the arithmetic: scores = cum + top_logprobs, masked to
@@ -101,3 +101,16 @@ def genrec_mask_topk_expand(cum, top_logprobs, top_tokens, select_k, node_ids=No
                     node_out[r, b] = transition(int(node_ids[r, int(par[b])]), int(tokens[r, b]),
                                                 next_node.long(), token_base, invalid_node)
     return vals, parents, tokens, indices, tok_out, node_out
+
+
+def row_topk(x: torch.Tensor, k: int, cand_ids: Optional[torch.Tensor] = None):
+    """Sorted per-row top-k with the candidate-id gather (scheduler.py:1476-1481,
+    graph.py:33-43): the stable descending sort's first k, i.e. equal scores
+    by ascending index, NaN first (torch's ordering).  Returns (vals, idx,
+    tokens) where tokens = cand_ids[idx] (idx when cand_ids is None)."""
+    x2 = x.float().reshape(-1, x.shape[-1])
+    vals, idx = torch.sort(x2, dim=-1, descending=True, stable=True)
+    vals, idx = vals[:, :k], idx[:, :k]
+    tokens = cand_ids.long()[idx] if cand_ids is not None else idx.clone()
+    shape = tuple(x.shape[:-1]) + (k,)
+    return vals.reshape(shape), idx.reshape(shape), tokens.reshape(shape)

@@ -92,3 +92,49 @@ def test_graph_replay_equals_eager(dev):
         out = m.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+def _small_beam(dev):
+    from flashrec_amd.decode_step import Qwen3FP8DecodeStep, Qwen3Shape
+
+    shape = Qwen3Shape(hidden=512, intermediate=1024, layers=2, q_heads=4, kv_heads=2,
+                       max_position=512, sid_tokens=512, vocab=2048)
+    return Qwen3FP8DecodeStep(shape, requests=2, beams=16, prefix=40, step=1, device=dev, seed=7,
+                              trie_items=500, trie_levels=3, trie_codes=64)
+
+
+def test_beam_tail_matches_oracle(dev):
+    """logprobs -> per-row top-2*BW over the SID head -> trie mask / top-BW /
+    expand / advance, against the oracle's composition on the same logprobs."""
+    from oracle import beam
+
+    m = _small_beam(dev)
+    lp = m.forward()
+    got = m.beam_step(lp)
+    tr = m.trie
+    n, bw, c = m.beam_n, m.beam_bw, m.beam_cand
+    assert c == 32
+    rv, _, rt = beam.row_topk(lp.cpu().view(n, bw, -1), c, m.cand_ids.cpu())
+    ref = beam.genrec_mask_topk_expand(m.beam_cum.cpu(), rv, rt, bw, m.beam_nodes.cpu(), tr["allow"].cpu(),
+                                       tr["base"], m.beam_tokens.cpu(), m.beam_col.cpu(),
+                                       tr["next"].cpu().long(), tr["invalid"])
+    for a, b in zip((got.vals, got.parents, got.tokens, got.indices, got.token_ids, got.node_ids), ref):
+        assert torch.equal(a.cpu(), b)
+    # every surviving pick is a level-1 code of the trie under its parent's node
+    ok = got.vals.cpu() > float("-inf")
+    assert ok.any()
+    rel = got.tokens.cpu() - tr["base"]
+    assert ((rel >= 64) & (rel < 128))[ok].all()
+
+
+def test_beam_graph_replay_equals_eager(dev):
+    m = _small_beam(dev)
+    eager = m.forward_beam()
+    ev = [t.clone() for t in (eager.vals, eager.tokens, eager.token_ids, eager.node_ids)]
+    m.capture(beam=True)
+    for _ in range(3):
+        torch.cuda.synchronize()
+        out = m.replay()
+        torch.cuda.synchronize()
+        for a, b in zip((out.vals, out.tokens, out.token_ids, out.node_ids), ev):
+            assert torch.equal(a, b)

@@ -30,7 +30,7 @@ def _decode_plan(lens, slots, seed):
 
 def test_single_key_returns_its_value():
     k, v = _pool(8, 2, 128, 0)
-    q = torch.randn(3, 4, 128).to(torch.bfloat16)
+    q = torch.randn(3, 4, 128, generator=torch.Generator().manual_seed(12)).to(torch.bfloat16)
     idx = torch.tensor([5, 2, 7], dtype=torch.int32)
     start = torch.tensor([0, 1, 2], dtype=torch.int32)
     ln = torch.ones(3, dtype=torch.int32)
@@ -44,7 +44,7 @@ def test_identical_keys_give_the_mean_value():
     """All keys equal -> uniform weights -> mean of V (any q)."""
     k, v = _pool(16, 1, 128, 1)
     k[:] = k[3]
-    q = torch.randn(1, 2, 128).to(torch.bfloat16) * 5
+    q = torch.randn(1, 2, 128, generator=torch.Generator().manual_seed(13)).to(torch.bfloat16) * 5
     idx = torch.arange(1, 11, dtype=torch.int32)
     out = ops.paged_attention(q, k, v, idx, torch.tensor([0], dtype=torch.int32),
                               torch.tensor([10], dtype=torch.int32), 0.3)
@@ -84,7 +84,7 @@ def test_grouped_query_heads_use_their_kv_head():
     hq, hk = 8, 2
     k, v = _pool(4, hk, 128, 4)
     v[:, 1] = (-v[:, 0].float()).to(E4M3)
-    q = torch.randn(1, hq, 128).to(torch.bfloat16)
+    q = torch.randn(1, hq, 128, generator=torch.Generator().manual_seed(14)).to(torch.bfloat16)
     out = ops.paged_attention(q, k, v, torch.tensor([3], dtype=torch.int32),
                               torch.tensor([0], dtype=torch.int32), torch.tensor([1], dtype=torch.int32), 0.1)
     for h in range(hq):
@@ -97,7 +97,7 @@ def test_matches_torch_sdpa_fp32(hq, hk):
     lens = [1, 5, 64, 130]
     k, v = _pool(512, hk, 128, 5)
     idx, indptr = _decode_plan(lens, 512, 6)
-    q = torch.randn(len(lens), hq, 128).to(torch.bfloat16)
+    q = torch.randn(len(lens), hq, 128, generator=torch.Generator().manual_seed(hq * 10 + hk)).to(torch.bfloat16)
     out = ops.paged_attention(q, k, v, idx, indptr[:-1].contiguous(), torch.tensor(lens, dtype=torch.int32),
                               128 ** -0.5)
     for i, n in enumerate(lens):
@@ -120,7 +120,7 @@ def test_matches_reference_bf16_call_sequence():
     lens = [3, 17, 129]
     k, v = _pool(256, 8, 128, 7)
     idx, indptr = _decode_plan(lens, 256, 8)
-    q = torch.randn(len(lens), 16, 128).to(torch.bfloat16)
+    q = torch.randn(len(lens), 16, 128, generator=torch.Generator().manual_seed(11)).to(torch.bfloat16)
     ours = ops.paged_attention(q, k, v, idx, indptr[:-1].contiguous(), torch.tensor(lens, dtype=torch.int32),
                                128 ** -0.5).float()
     ref = ops.sdpa_reference_style(q, k, v, idx, indptr).float()

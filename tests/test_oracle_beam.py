@@ -96,3 +96,29 @@ def test_trie_rules():
     assert beam.transition(0, 11, nxt, 10, -1) == 6
     assert beam.transition(0, 12, nxt, 10, -1) == -1   # outside -> invalid
     assert beam.transition(7, 10, nxt, 10, -1) == 5    # node clamped to the table
+
+
+def test_row_topk_matches_torch_topk_without_ties():
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(6, 300, generator=g)
+    assert x.unique().numel() == x.numel()
+    cand = torch.arange(1000, 1300)
+    for k in (1, 17, 300):
+        vals, idx, tok = beam.row_topk(x, k, cand)
+        tv, ti = torch.topk(x, k, dim=-1, largest=True, sorted=True)
+        assert torch.equal(vals, tv) and torch.equal(idx, ti)
+        assert torch.equal(tok, ti + 1000)
+
+
+def test_row_topk_ties_nan_and_signed_zero_by_hand():
+    nan, inf = float("nan"), float("inf")
+    x = torch.tensor([[0.0, -0.0, 1.0, nan, -inf, 1.0, inf, nan, -0.0]])
+    vals, idx, tok = beam.row_topk(x, 9)
+    # NaN first (by index), then +inf, the 1.0 tie by index, the three zeros
+    # (signed zero equal) by index, then -inf
+    assert idx.tolist() == [[3, 7, 6, 2, 5, 0, 1, 8, 4]]
+    assert torch.equal(tok, idx)
+    assert torch.isnan(vals[0, :2]).all()
+    assert vals[0, 2:].tolist() == [inf, 1.0, 1.0, 0.0, -0.0, -0.0, -inf]
+    _, idx3, _ = beam.row_topk(x, 3)
+    assert idx3.tolist() == [[3, 7, 6]]
