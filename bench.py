@@ -112,8 +112,9 @@ def _decode_step_case(dev):
     from flashrec_amd.decode_step import Qwen3FP8DecodeStep, Qwen3Shape
 
     shape = Qwen3Shape()
-    m = Qwen3FP8DecodeStep(shape, requests=8, beams=512, prefix=128, step=2, device=dev)
-    m.capture()
+    m = Qwen3FP8DecodeStep(shape, requests=8, beams=512, prefix=128, step=2, device=dev,
+                           trie_items=200000, trie_levels=3, trie_codes=256)
+    m.capture(beam=True)
     for _ in range(3):
         m.replay()
     torch.cuda.synchronize()
@@ -134,7 +135,13 @@ def _decode_step_case(dev):
         "ms": round(ms, 4), "GEMM_TFLOP/s": round(gemm_flops / (ms * 1e-3) / 1e12, 1),
         "gemm_tflop_per_step": round(gemm_flops / 1e12, 3), "layers": shape.layers, "rows": rows,
         "kv_len": m.seq_len, "timing": "one HIP graph per step, mean of 10 replays",
-        "excludes": "trie mask / top-k / beam expand (separate kernel)"}}
+        "includes": "28 layers, fp8 SID lm_head + log_softmax, per-row top-1024 candidates, "
+                    "3-level x 256 trie mask + top-512 per request + expand/advance",
+        "trie_nodes": m.trie["n_nodes"]}}
+    lp = torch.log_softmax(torch.randn(rows, shape.sid_tokens, device=dev), dim=-1)
+    ms_b = _graph_timed(lambda _i: m.beam_step(lp), 1)
+    out["config4_beam_tail"] = {"ms": round(ms_b, 5), "rows": rows, "candidates_per_row": m.beam_cand,
+                                "select_k": m.beam_bw, "kernels": "row_topk + genrec (2 kernels)"}
     p = m.attn._plan
     q = torch.randn(rows, shape.q_heads, shape.head_dim, device=dev).to(torch.bfloat16)
     o = torch.empty_like(q)
