@@ -159,8 +159,10 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   constexpr int STAGE = (BN + BM) * kBK;
   constexpr int LOADS = IB + IA;  // vmcnt units one K step adds per wave
   constexpr int EB = OutT<OUT>::kBytes;
-  constexpr int STG = 32 * 256;  // epilogue staging per wave: 32 rows x 64 fp32
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * STAGE + 4 * STG];
+  constexpr int STG = 32 * 128;  // epilogue staging per wave: 32 rows x 128 bytes
+  // LDS: the K-step ring, per-wave epilogue staging, two 2 KB scale buffers
+  // LDS: the K-step ring, per-wave epilogue staging, two 2 KB scale buffers
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * STAGE + 4 * STG + 2 * 2048];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -193,23 +195,24 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   const int lrow = lane >> 2;
   const int lchunk = (lane & 3) ^ swz_g(lrow);
   constexpr uint32_t kOOB = 0x80000000u;
-  uint32_t ob_cur[IB], oa_cur[IA], ob_nxt[IB], oa_nxt[IA];
-  auto tile_offsets = [&](int64_t local, uint32_t* ob, uint32_t* oa) __attribute__((always_inline)) {
+  // Per-lane part of each load's offset (the same for every tile) and the
+  // scalar tile bases of the current and the next tile; a tile past the end
+  // gets base kOOB (the sum is then past the buffer: zeros, no access).
+  uint32_t lob[IB], loa[IA];
+#pragma unroll
+  for (int i = 0; i < IB; ++i) lob[i] = static_cast<uint32_t>(((i * 4 + wave) * 16 + lrow) * g.ldb + lchunk * 16);
+#pragma unroll
+  for (int i = 0; i < IA; ++i) loa[i] = static_cast<uint32_t>(((i * 4 + wave) * 16 + lrow) * g.lda + lchunk * 16);
+  uint32_t bb_cur, ba_cur, bb_nxt, ba_nxt;
+  auto tile_bases = [&](int64_t local, uint32_t& bb, uint32_t& ba) __attribute__((always_inline)) {
     if (local >= my_tiles) {
-#pragma unroll
-      for (int i = 0; i < IB; ++i) ob[i] = kOOB;
-#pragma unroll
-      for (int i = 0; i < IA; ++i) oa[i] = kOOB;
+      bb = ba = kOOB;
       return;
     }
     int64_t tm, tn;
     tile_coords(blockIdx.x + local * G, nt, tilesM, tm, tn);
-#pragma unroll
-    for (int i = 0; i < IB; ++i)
-      ob[i] = static_cast<uint32_t>((tn * BN + (i * 4 + wave) * 16 + lrow) * g.ldb + lchunk * 16);
-#pragma unroll
-    for (int i = 0; i < IA; ++i)
-      oa[i] = static_cast<uint32_t>((tm * BM + (i * 4 + wave) * 16 + lrow) * g.lda + lchunk * 16);
+    bb = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(tn * BN * g.ldb));
+    ba = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(tm * BM * g.lda));
   };
   // Load `l` (0..LOADS-1: weight blocks, then activation blocks) of K step
   // `lk` (0..KT-1) of the cur or nxt tile into `slot`.
@@ -219,12 +222,12 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     const uint32_t k0 = static_cast<uint32_t>(lk) * kBK;
     const bool kin = !KTAIL || (k0 + lchunk * 16 < static_cast<uint64_t>(g.K));
     if (l < IB) {
-      const uint32_t o = next ? ob_nxt[l] : ob_cur[l];
+      const uint32_t o = lob[l] + (next ? bb_nxt : bb_cur);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(sb + (l * 4 + wave) * 1024), 16,
                                                kin ? o : kOOB, k0, 0, 0);
     } else {
       const int i = l - IB;
-      const uint32_t o = next ? oa_nxt[i] : oa_cur[i];
+      const uint32_t o = loa[i] + (next ? ba_nxt : ba_cur);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(sa + (i * 4 + wave) * 1024), 16,
                                                kin ? o : kOOB, k0, 0, 0);
     }
@@ -237,10 +240,20 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   // ---- fragments and MFMAs
   const int fr = lane & 31;        // fragment row inside a 32-row block
   const int c0 = (lane >> 5) * 2;  // first 16-byte chunk of this lane's 32 bytes
-  // Fragments as 16-byte halves: read r (0..2*(FN+FM)-1) fills half r%2 of
-  // weight block r/2, then of activation block r/2 - FN.
+  // Fragments as 16-byte halves.  Activation fragments are used by every
+  // MFMA row and have two register sets (current step, next step).  Weight
+  // fragments have two sets too, except on the 256x256 tile, where registers
+  // are short: there block i of the next step is read right after the last
+  // MFMA that uses block i of the current one.  Read r (0..2*(FN+FM)-1) fills
+  // half r%2 of weight block r/2, then of activation block r/2 - FN.
+  constexpr bool kOneB = BN == 256 && BM == 256;
   struct Frags {
     u32x4 b[FN][2], a[FM][2];
+  };
+  u32x4 fb1[kOneB ? FN : 1][2];  // the single weight set (kOneB)
+  auto breg = [&](Frags& f, int i, int h) -> u32x4& __attribute__((always_inline)) {
+    if constexpr (kOneB) return fb1[i][h];
+    else return f.b[i][h];
   };
   auto read_one = [&](Frags& f, int slot, int r) __attribute__((always_inline)) {
     const uint8_t* sb = smem + slot * STAGE;
@@ -248,7 +261,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     const int h = r & 1;
     if (r < 2 * FN) {
       const int i = r >> 1;
-      f.b[i][h] = *reinterpret_cast<const u32x4*>(sb + swz(wn * WN + i * 32 + fr, c0 + h));
+      breg(f, i, h) = *reinterpret_cast<const u32x4*>(sb + swz(wn * WN + i * 32 + fr, c0 + h));
     } else {
       const int j = (r >> 1) - FN;
       f.a[j][h] = *reinterpret_cast<const u32x4*>(sa + swz(wm * WM + j * 32 + fr, c0 + h));
@@ -267,47 +280,47 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
   };
-  auto mfma_one = [&](const Frags& f, int i, int j) __attribute__((always_inline)) {
-    const v8i bv = (v8i)__builtin_shufflevector(f.b[i][0], f.b[i][1], 0, 1, 2, 3, 4, 5, 6, 7);
+  auto mfma_one = [&](Frags& f, int i, int j) __attribute__((always_inline)) {
+    const v8i bv = (v8i)__builtin_shufflevector(breg(f, i, 0), breg(f, i, 1), 0, 1, 2, 3, 4, 5, 6, 7);
     const v8i av = (v8i)__builtin_shufflevector(f.a[j][0], f.a[j][1], 0, 1, 2, 3, 4, 5, 6, 7);
     acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, acc[i][j], 0, 0, 0, 0, 0, 0);
   };
 
   // ---- epilogue of one tile.  Lane l holds, per block (i, j), output row
   // m = l%32 of block j and the 4 consecutive columns n = 8q + 4(l/32) + t of
-  // block i (q, t = 0..3).  Fast path: acc * sa[m] goes to an fp32 staging
-  // tile of 32 rows x 64 columns per pass (16-byte chunk c of row r at slot
-  // c ^ (r % 16)), is read back as 8 consecutive columns per lane, multiplied
-  // by sb[n], converted and stored as whole row segments.  The scales of the
-  // tile are loaded into registers when the tile starts (load_scales), so the
-  // epilogue issues no global load: any load here would have to wait behind
-  // the next tile's ring loads (vmcnt retires in order).
-  constexpr int PCOLS = 64;                          // fp32 staging columns per pass
+  // block i (q, t = 0..3).  Fast path: (acc * sa[m]) * sb[n] is converted and
+  // written to a per-wave staging tile of 32 rows x 128 bytes per pass (16-byte
+  // chunk c of row r at slot c ^ (r % 8)), read back as 16 consecutive bytes
+  // per lane and stored as whole 128-byte row segments.  The tile's scales
+  // are brought into LDS by direct loads when the tile starts (load_scales),
+  // so the epilogue issues no global load (a load here would queue behind
+  // the next tile's ring loads: vmcnt retires in order) and holds no scale
+  // registers through the K loop.
+  constexpr int PCOLS = 128 / EB;  // output columns per staging pass
   constexpr int PASSES = WN / PCOLS;
+  constexpr int BPP = PCOLS / 32;  // 32-column blocks per pass
   static_assert(WN % PCOLS == 0, "wave tile width");
   uint8_t* stg = smem + NST * STAGE + wave * STG;
-  float sa_r[FM];
-  float sb_r[PASSES][8];
+  uint8_t* const scl = smem + NST * STAGE + 4 * STG;
+  // scales: sb[BN] (1 KB) then sa[BM] (1 KB) as fp32, one buffer per tile parity
+  const bool sa_vec = g.sa_stride != 0, sb_vec = g.sb_stride != 0;
+  const __amdgpu_buffer_rsrc_t rsa = make_rsrc(g.sa, static_cast<uint32_t>(g.M * 4));
+  const __amdgpu_buffer_rsrc_t rsb = make_rsrc(g.sb, static_cast<uint32_t>(g.N * 4));
+  // per-tensor scales, read once up front (never a load in the epilogue)
+  const float sa0 = sa_vec ? 0.0f : __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(g.sa[0])));
+  const float sb0 = sb_vec ? 0.0f : __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(g.sb[0])));
   auto load_scales = [&](int64_t local) __attribute__((always_inline)) {
     if (local >= my_tiles) return;
     int64_t tm, tn;
     tile_coords(blockIdx.x + local * G, nt, tilesM, tm, tn);
-    const int64_t m0 = tm * BM + wm * WM;
-    const int64_t n0 = tn * BN + wn * WN;
-#pragma unroll
-    for (int j = 0; j < FM; ++j) {
-      int64_t m = m0 + j * 32 + (lane & 31);
-      m = m < g.M ? m : g.M - 1;
-      sa_r[j] = g.sa[m * g.sa_stride];
-    }
-#pragma unroll
-    for (int p = 0; p < PASSES; ++p)
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        int64_t n = n0 + p * PCOLS + (lane & 7) * 8 + t;
-        n = n < g.N ? n : g.N - 1;
-        sb_r[p][t] = g.sb[n * g.sb_stride];
-      }
+    uint8_t* dst = scl + (local & 1) * 2048;
+    const uint32_t l16 = 16 * __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    if (wave == 0 && sb_vec)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_ptr_t)dst, 16,
+                                               static_cast<uint32_t>(tn * BN * 4) + l16, 0, 0, 0);
+    if (wave == 1 && sa_vec)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_ptr_t)(dst + 1024), 16,
+                                               static_cast<uint32_t>(tm * BM * 4) + l16, 0, 0, 0);
   };
   auto epilogue = [&](int64_t local) __attribute__((always_inline)) {
     int64_t tm, tn;
@@ -339,47 +352,50 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
       }
       return;
     }
+    const float* sbl = reinterpret_cast<const float*>(scl + (local & 1) * 2048) + wn * WN;
+    const float* sal = reinterpret_cast<const float*>(scl + (local & 1) * 2048 + 1024) + wm * WM;
+    // lane-derived addresses are formed here from a freshly computed lane id,
+    // not hoisted out of the tile loop (held across it they would be
+    // spilled, and the reloads' vmcnt waits would drain the load ring)
+    const int lx = static_cast<int>(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)));
+    const int row = lx & 31;
 #pragma unroll
     for (int j = 0; j < FM; ++j) {
+      const float sam = sa_vec ? sal[j * 32 + row] : sa0;
 #pragma unroll
       for (int p = 0; p < PASSES; ++p) {
-        const int row = lane & 31;
 #pragma unroll
-        for (int ii = 0; ii < PCOLS / 32; ++ii) {
-          const int i = p * (PCOLS / 32) + ii;
+        for (int ii = 0; ii < BPP; ++ii) {
+          const int i = p * BPP + ii;
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const int chunk = ii * 8 + 2 * q + (lane >> 5);  // 16-byte chunk of the pass row
-            float4 v = make_float4(acc[i][j][4 * q + 0] * sa_r[j], acc[i][j][4 * q + 1] * sa_r[j],
-                                   acc[i][j][4 * q + 2] * sa_r[j], acc[i][j][4 * q + 3] * sa_r[j]);
-            *reinterpret_cast<float4*>(stg + row * 256 + ((chunk ^ (row & 15)) << 4)) = v;
+            const int col = ii * 32 + 8 * q + 4 * (lx >> 5);  // column inside the pass
+            float4 sbv = make_float4(sb0, sb0, sb0, sb0);
+            if (sb_vec) sbv = *reinterpret_cast<const float4*>(sbl + i * 32 + 8 * q + 4 * (lx >> 5));
+            const float v0 = (acc[i][j][4 * q + 0] * sam) * sbv.x;
+            const float v1 = (acc[i][j][4 * q + 1] * sam) * sbv.y;
+            const float v2 = (acc[i][j][4 * q + 2] * sam) * sbv.z;
+            const float v3 = (acc[i][j][4 * q + 3] * sam) * sbv.w;
+            const int byte = col * EB;
+            uint8_t* d = stg + row * 128 + ((((byte >> 4) ^ (row & 7))) << 4) + (byte & 15);
+            if (OUT == FR_DTYPE_FP32) {
+              *reinterpret_cast<float4*>(d) = make_float4(v0, v1, v2, v3);
+            } else {
+              uint2 w;
+              w.x = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v0, v1) : pack_fp16x2(v0, v1);
+              w.y = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v2, v3) : pack_fp16x2(v2, v3);
+              *reinterpret_cast<uint2*>(d) = w;
+            }
           }
         }
-        // read back: 8 lanes per row, 8 consecutive columns per lane
+        // read back: 8 lanes per 128-byte row, 8 rows per instruction
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
-          const int r = rr * 8 + (lane >> 3);
-          const int cg = lane & 7;
-          const float4 x0 =
-              *reinterpret_cast<const float4*>(stg + r * 256 + (((2 * cg) ^ (r & 15)) << 4));
-          const float4 x1 =
-              *reinterpret_cast<const float4*>(stg + r * 256 + (((2 * cg + 1) ^ (r & 15)) << 4));
-          const float v[8] = {x0.x * sb_r[p][0], x0.y * sb_r[p][1], x0.z * sb_r[p][2],
-                              x0.w * sb_r[p][3], x1.x * sb_r[p][4], x1.y * sb_r[p][5],
-                              x1.z * sb_r[p][6], x1.w * sb_r[p][7]};
-          const int64_t off = (m0 + j * 32 + r) * g.ldo + n0 + p * PCOLS + cg * 8;
-          if (OUT == FR_DTYPE_FP32) {
-            float* o = static_cast<float*>(g.out) + off;
-            *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
-            *reinterpret_cast<float4*>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
-          } else {
-            u32x4 w;
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-              w[t] = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v[2 * t], v[2 * t + 1])
-                                          : pack_fp16x2(v[2 * t], v[2 * t + 1]);
-            *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(g.out) + off) = w;
-          }
+          const int r = rr * 8 + (lx >> 3);
+          const int cg = lx & 7;
+          const u32x4 w = *reinterpret_cast<const u32x4*>(stg + r * 128 + ((cg ^ (r & 7)) << 4));
+          const int64_t off = (m0 + j * 32 + r) * g.ldo + n0 + p * PCOLS + cg * (16 / EB);
+          *reinterpret_cast<u32x4*>(static_cast<uint8_t*>(g.out) + off * EB) = w;
         }
       }
     }
@@ -389,8 +405,8 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   // With more than one tile per workgroup KT >= NST (see launch_mfma), so
   // the prologue stays inside tile 0; with one tile, steps past its end are
   // all-zero dummies.
-  tile_offsets(0, ob_cur, oa_cur);
-  tile_offsets(1, ob_nxt, oa_nxt);
+  tile_bases(0, bb_cur, ba_cur);
+  tile_bases(1, bb_nxt, ba_nxt);
   load_scales(0);
 #pragma unroll
   for (int st = 0; st < NST; ++st) issue(st, st < KT ? st : st - KT, st >= KT);
@@ -434,16 +450,28 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     const bool nx = lk0 >= KT;
     const int slot = static_cast<int>(s % NST);
     const int nslot = static_cast<int>((s + 1) % NST);
-    // Unit u: its share of step s+1's fragment reads, MFMA u of step s, its
-    // share of the refill loads.  The sched_barrier keeps units in order, so
-    // the loads leave at the rate the step consumes data and the wave never
-    // stalls on a full load queue while it has MFMAs to issue.
+    // Unit u: its share of step s+1's fragment reads, MFMA u of step s
+    // (weight block u / FM), with a single weight set the next weight block's
+    // reads once its last MFMA is issued, its share of the refill loads.  The
+    // sched_barrier keeps units in order, so the loads leave at the rate the
+    // step consumes data and the wave never stalls on a full load queue while
+    // it has MFMAs to issue.
 #pragma unroll
     for (int u = 0; u < NMF; ++u) {
+      if constexpr (kOneB) {
 #pragma unroll
-      for (int r = 0; r < NRD; ++r)
-        if (r * RDU / NRD == u) read_one(nxt, nslot, r);
+        for (int r = 0; r < 2 * FM; ++r)
+          if (r * RDU / (2 * FM) == u) read_one(nxt, nslot, 2 * FN + r);
+      } else {
+#pragma unroll
+        for (int r = 0; r < NRD; ++r)
+          if (r * RDU / NRD == u) read_one(nxt, nslot, r);
+      }
       mfma_one(cur, u / FM, u % FM);
+      if (kOneB && u % FM == FM - 1) {
+        read_one(nxt, nslot, 2 * (u / FM));
+        read_one(nxt, nslot, 2 * (u / FM) + 1);
+      }
 #pragma unroll
       for (int l = 0; l < LOADS; ++l)
         if (LD0 + l * (NMF - LD0) / LOADS == u) issue_one(slot, lk, nx, l);
@@ -463,11 +491,9 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     epilogue(tile);
     zero_acc();
     load_scales(tile + 1);
-#pragma unroll
-    for (int i = 0; i < IB; ++i) ob_cur[i] = ob_nxt[i];
-#pragma unroll
-    for (int i = 0; i < IA; ++i) oa_cur[i] = oa_nxt[i];
-    tile_offsets(tile + 2, ob_nxt, oa_nxt);
+    bb_cur = bb_nxt;
+    ba_cur = ba_nxt;
+    tile_bases(tile + 2, bb_nxt, ba_nxt);
   }
   waitcnt_vm<0>();  // drain the trailing dummy loads before the LDS is released
 #endif  // __HIP_DEVICE_COMPILE__
