@@ -86,6 +86,86 @@ __device__ __forceinline__ void waitcnt_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// LDS accesses of the epilogue, written as inline asm: the compiler cannot
+// tell plain LDS accesses from the ring's direct-to-LDS writes, so before each
+// one it would wait for vmcnt(0) -- all ring loads and every output store
+// issued so far.  These need no such wait (the scales landed long before, and
+// the staging area is never a direct-load target); the reads carry their own
+// lgkmcnt wait.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
+}
+__device__ __forceinline__ void lds_write_b64(uint32_t a, uint32_t lo, uint32_t hi) {
+  asm volatile("ds_write_b64 %0, %1" ::"v"(a), "v"(make_uint2(lo, hi)) : "memory");
+}
+__device__ __forceinline__ void lds_write_b128(uint32_t a, u32x4 v) {
+  asm volatile("ds_write_b128 %0, %1" ::"v"(a), "v"(v) : "memory");
+}
+// four 16-byte reads, then the wait for all of them
+__device__ __forceinline__ void lds_read4_b128(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3,
+                                               u32x4& r0, u32x4& r1, u32x4& r2, u32x4& r3) {
+  asm volatile(
+      "ds_read_b128 %0, %4\n\tds_read_b128 %1, %5\n\tds_read_b128 %2, %6\n\tds_read_b128 %3, %7\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
+      : "v"(a0), "v"(a1), "v"(a2), "v"(a3)
+      : "memory");
+}
+// Reads without their wait; lds_wait_all() then retires them all and, by
+// taking the registers as operands, keeps every use after it.
+__device__ __forceinline__ u32x4 lds_read_b128_nw(uint32_t a) {
+  u32x4 r;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(a) : "memory");
+  return r;
+}
+__device__ __forceinline__ float lds_read_f32_nw(uint32_t a) {
+  float r;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(a) : "memory");
+  return r;
+}
+template <int NV, int NF>
+__device__ __forceinline__ void lds_wait_all(u32x4 (&v)[NV], float (&f)[NF]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < NV; ++i) asm volatile("" : "+v"(v[i]));
+#pragma unroll
+  for (int i = 0; i < NF; ++i) asm volatile("" : "+v"(f[i]));
+}
+__device__ __forceinline__ float lds_read_f32(uint32_t a) {
+  float r;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(a) : "memory");
+  return r;
+}
+
+// Lane id, computed where it is written (a volatile asm is never hoisted
+// out of the tile loop, where holding it would cost a register).
+__device__ __forceinline__ int lane_id_here() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
+// A 16-byte-per-lane direct-to-LDS load written as inline asm, for the tile
+// scales: issued through the builtin, the compiler would treat every later
+// LDS read as possibly aliasing it and wait for vmcnt(0) first -- at the
+// next tile's first fragment read, that is for all of the previous tile's
+// output stores.  The K loop's own waits cover this load.
+typedef int v4i __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void lds_dma_b128(const void* base, uint32_t bytes, uint32_t lds_dst,
+                                             uint32_t voff) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  v4i rs;
+  rs[0] = static_cast<int>(b & 0xFFFFFFFFu);
+  rs[1] = static_cast<int>((b >> 32) & 0xFFFFu);
+  rs[2] = static_cast<int>(bytes);
+  rs[3] = 0x00020000;
+  rs[0] = __builtin_amdgcn_readfirstlane(rs[0]);
+  rs[1] = __builtin_amdgcn_readfirstlane(rs[1]);
+  rs[2] = __builtin_amdgcn_readfirstlane(rs[2]);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :: "s"(lds_dst), "v"(voff), "s"(rs) : "memory", "m0");
+}
+
 // Raw buffer resource over [base, base + bytes): loads past the end return 0.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
@@ -159,10 +239,10 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   constexpr int STAGE = (BN + BM) * kBK;
   constexpr int LOADS = IB + IA;  // vmcnt units one K step adds per wave
   constexpr int EB = OutT<OUT>::kBytes;
+  // LDS: the K-step ring, per-wave epilogue staging, two 2 KB scale buffers
   constexpr int STG = 32 * 128;  // epilogue staging per wave: 32 rows x 128 bytes
-  // LDS: the K-step ring, per-wave epilogue staging, two 2 KB scale buffers
-  // LDS: the K-step ring, per-wave epilogue staging, two 2 KB scale buffers
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * STAGE + 4 * STG + 2 * 2048];
+  // LDS: the K-step ring, two 2 KB scale buffers, per-wave epilogue staging
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * STAGE + 2 * 2048 + 4 * STG];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -296,16 +376,10 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   // so the epilogue issues no global load (a load here would queue behind
   // the next tile's ring loads: vmcnt retires in order) and holds no scale
   // registers through the K loop.
-  constexpr int PCOLS = 128 / EB;  // output columns per staging pass
-  constexpr int PASSES = WN / PCOLS;
-  constexpr int BPP = PCOLS / 32;  // 32-column blocks per pass
-  static_assert(WN % PCOLS == 0, "wave tile width");
-  uint8_t* stg = smem + NST * STAGE + wave * STG;
-  uint8_t* const scl = smem + NST * STAGE + 4 * STG;
+  uint8_t* const scl = smem + NST * STAGE;
+  uint8_t* const stg = smem + NST * STAGE + 2 * 2048 + wave * STG;
   // scales: sb[BN] (1 KB) then sa[BM] (1 KB) as fp32, one buffer per tile parity
   const bool sa_vec = g.sa_stride != 0, sb_vec = g.sb_stride != 0;
-  const __amdgpu_buffer_rsrc_t rsa = make_rsrc(g.sa, static_cast<uint32_t>(g.M * 4));
-  const __amdgpu_buffer_rsrc_t rsb = make_rsrc(g.sb, static_cast<uint32_t>(g.N * 4));
   // per-tensor scales, read once up front (never a load in the epilogue)
   const float sa0 = sa_vec ? 0.0f : __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(g.sa[0])));
   const float sb0 = sb_vec ? 0.0f : __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(g.sb[0])));
@@ -314,15 +388,23 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     int64_t tm, tn;
     tile_coords(blockIdx.x + local * G, nt, tilesM, tm, tn);
     uint8_t* dst = scl + (local & 1) * 2048;
-    const uint32_t l16 = 16 * __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    const uint32_t l16 = 16 * lane_id_here();
     if (wave == 0 && sb_vec)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_ptr_t)dst, 16,
-                                               static_cast<uint32_t>(tn * BN * 4) + l16, 0, 0, 0);
+      lds_dma_b128(g.sb, static_cast<uint32_t>(g.N * 4), lds_addr(dst), static_cast<uint32_t>(tn * BN * 4) + l16);
     if (wave == 1 && sa_vec)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_ptr_t)(dst + 1024), 16,
-                                               static_cast<uint32_t>(tm * BM * 4) + l16, 0, 0, 0);
+      lds_dma_b128(g.sa, static_cast<uint32_t>(g.M * 4), lds_addr(dst + 1024),
+                   static_cast<uint32_t>(tm * BM * 4) + l16);
   };
-  auto epilogue = [&](int64_t local) __attribute__((always_inline)) {
+  // bf16/fp16 outputs leave the epilogue through an LDS staging tile as
+  // 16-byte row segments.  8-byte stores straight from the accumulator
+  // layout (kDirectStores) need no LDS round trips but twice the store
+  // instructions; measured in one process against the staged form, they were
+  // 1-12 % slower on every tile shape, so they are off.
+  constexpr bool kDirectStores = false;
+  constexpr int kStagedStores = kDirectStores ? 4 * FN * FM : 2 * FN * FM;  // stores per wave per tile
+  // Returns whether the bf16/fp16 fast path ran (and so issued exactly
+  // kStagedStores stores per wave).
+  auto epilogue = [&](int64_t local) -> bool __attribute__((always_inline)) {
     int64_t tm, tn;
     tile_coords(blockIdx.x + local * G, nt, tilesM, tm, tn);
     const int64_t m0 = tm * BM + wm * WM;
@@ -350,55 +432,121 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
             store4<OUT>(g.out, g.ldo, m, n, g.N, v, g.bias);
           }
       }
-      return;
+      return false;
     }
-    const float* sbl = reinterpret_cast<const float*>(scl + (local & 1) * 2048) + wn * WN;
-    const float* sal = reinterpret_cast<const float*>(scl + (local & 1) * 2048 + 1024) + wm * WM;
-    // lane-derived addresses are formed here from a freshly computed lane id,
+    // lane-derived values are formed here from a freshly computed lane id,
     // not hoisted out of the tile loop (held across it they would be
-    // spilled, and the reloads' vmcnt waits would drain the load ring)
-    const int lx = static_cast<int>(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)));
+    // spilled, and a reload's vmcnt wait would drain the load ring)
+    const int lx = lane_id_here();
     const int row = lx & 31;
+    const int h4 = 4 * (lx >> 5);
+    const uint32_t sbl = lds_addr(scl + (local & 1) * 2048) + 4 * (wn * WN + h4);
+    const uint32_t sal = lds_addr(scl + (local & 1) * 2048 + 1024) + 4 * (wm * WM + row);
+    if (OUT == FR_DTYPE_FP32) {
+      // 16 bytes per lane already: (i, j, q) -> row l%32, 4 columns
 #pragma unroll
-    for (int j = 0; j < FM; ++j) {
-      const float sam = sa_vec ? sal[j * 32 + row] : sa0;
+      for (int j = 0; j < FM; ++j) {
+        const float sam = sa_vec ? lds_read_f32(sal + 128 * j) : sa0;
+        float* orow = static_cast<float*>(g.out) + (m0 + j * 32 + row) * g.ldo + n0 + h4;
 #pragma unroll
-      for (int p = 0; p < PASSES; ++p) {
-#pragma unroll
-        for (int ii = 0; ii < BPP; ++ii) {
-          const int i = p * BPP + ii;
+        for (int i = 0; i < FN; ++i) {
+          u32x4 sb4[4];
+          if (sb_vec) lds_read4_b128(sbl + 128 * i, sbl + 128 * i + 32, sbl + 128 * i + 64, sbl + 128 * i + 96,
+                                     sb4[0], sb4[1], sb4[2], sb4[3]);
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const int col = ii * 32 + 8 * q + 4 * (lx >> 5);  // column inside the pass
-            float4 sbv = make_float4(sb0, sb0, sb0, sb0);
-            if (sb_vec) sbv = *reinterpret_cast<const float4*>(sbl + i * 32 + 8 * q + 4 * (lx >> 5));
-            const float v0 = (acc[i][j][4 * q + 0] * sam) * sbv.x;
-            const float v1 = (acc[i][j][4 * q + 1] * sam) * sbv.y;
-            const float v2 = (acc[i][j][4 * q + 2] * sam) * sbv.z;
-            const float v3 = (acc[i][j][4 * q + 3] * sam) * sbv.w;
-            const int byte = col * EB;
-            uint8_t* d = stg + row * 128 + ((((byte >> 4) ^ (row & 7))) << 4) + (byte & 15);
-            if (OUT == FR_DTYPE_FP32) {
-              *reinterpret_cast<float4*>(d) = make_float4(v0, v1, v2, v3);
-            } else {
-              uint2 w;
-              w.x = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v0, v1) : pack_fp16x2(v0, v1);
-              w.y = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v2, v3) : pack_fp16x2(v2, v3);
-              *reinterpret_cast<uint2*>(d) = w;
-            }
+            float v[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              v[t] = (acc[i][j][4 * q + t] * sam) * (sb_vec ? __uint_as_float(sb4[q][t]) : sb0);
+            *reinterpret_cast<float4*>(orow + i * 32 + 8 * q) = make_float4(v[0], v[1], v[2], v[3]);
           }
         }
-        // read back: 8 lanes per 128-byte row, 8 rows per instruction
+      }
+      return false;
+    }
+    // bf16 / fp16: per pass (j, two column blocks) the converted outputs go
+    // to a 32 x 128-byte staging tile (16-byte chunk c of row r at slot
+    // c ^ (r % 8)), are read back as 16 consecutive bytes per lane and stored
+    // as 128-byte row segments: 16 KB a store instruction per 8 rows.  All
+    // scales are read up front, in one LDS round trip.
+    const uint32_t stg_base = lds_addr(stg);
+    u32x4 sb4[FN * 4];
+    float sam_r[FM];
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int r = rr * 8 + (lx >> 3);
+    for (int j = 0; j < FM; ++j) sam_r[j] = sa_vec ? lds_read_f32_nw(sal + 128 * j) : sa0;
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (sb_vec) {
+          sb4[4 * i + q] = lds_read_b128_nw(sbl + 128 * i + 32 * q);
+        } else {
+          const uint32_t b0 = __float_as_uint(sb0);
+          sb4[4 * i + q] = u32x4{b0, b0, b0, b0};
+        }
+      }
+    lds_wait_all(sb4, sam_r);
+    if constexpr (kDirectStores) {
+      // stores straight from the accumulator layout: lane l writes the 4
+      // outputs (8 bytes) of row l%32, columns 8q + 4(l/32) .. +3 of each block
+  #pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        const float sam = sam_r[j];
+        uint16_t* orow = static_cast<uint16_t*>(g.out) + (m0 + j * 32 + row) * g.ldo + n0 + h4;
+  #pragma unroll
+        for (int i = 0; i < FN; ++i)
+  #pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float v[4];
+  #pragma unroll
+            for (int t = 0; t < 4; ++t) v[t] = (acc[i][j][4 * q + t] * sam) * __uint_as_float(sb4[4 * i + q][t]);
+            uint2 w;
+            w.x = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v[0], v[1]) : pack_fp16x2(v[0], v[1]);
+            w.y = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v[2], v[3]) : pack_fp16x2(v[2], v[3]);
+            *reinterpret_cast<uint2*>(orow + i * 32 + 8 * q) = w;
+          }
+      }
+    } else {
+  #pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        const float sam = sam_r[j];
+  #pragma unroll
+        for (int p = 0; p < FN / 2; ++p) {
+  #pragma unroll
+          for (int ii = 0; ii < 2; ++ii) {
+            const int i = 2 * p + ii;
+  #pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              float v[4];
+  #pragma unroll
+              for (int t = 0; t < 4; ++t) v[t] = (acc[i][j][4 * q + t] * sam) * __uint_as_float(sb4[4 * i + q][t]);
+              const uint32_t lo = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v[0], v[1]) : pack_fp16x2(v[0], v[1]);
+              const uint32_t hi = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v[2], v[3]) : pack_fp16x2(v[2], v[3]);
+              const int byte = 2 * (ii * 32 + 8 * q + h4);  // inside the 128-byte staging row
+              lds_write_b64(stg_base + row * 128 + ((((byte >> 4) ^ (row & 7))) << 4) + (byte & 15), lo, hi);
+            }
+          }
+          // read back: 8 lanes per 128-byte row, 8 rows per read
           const int cg = lx & 7;
-          const u32x4 w = *reinterpret_cast<const u32x4*>(stg + r * 128 + ((cg ^ (r & 7)) << 4));
-          const int64_t off = (m0 + j * 32 + r) * g.ldo + n0 + p * PCOLS + cg * (16 / EB);
-          *reinterpret_cast<u32x4*>(static_cast<uint8_t*>(g.out) + off * EB) = w;
+          uint32_t ra[4];
+          int rr_row[4];
+  #pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            rr_row[rr] = rr * 8 + (lx >> 3);
+            ra[rr] = stg_base + rr_row[rr] * 128 + ((cg ^ (rr_row[rr] & 7)) << 4);
+          }
+          u32x4 w[4];
+          lds_read4_b128(ra[0], ra[1], ra[2], ra[3], w[0], w[1], w[2], w[3]);
+  #pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            const int64_t off = (m0 + j * 32 + rr_row[rr]) * g.ldo + n0 + p * 64 + cg * 8;
+            *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(g.out) + off) = w[rr];
+          }
         }
       }
     }
+    return true;
   };
 
   // ---- prologue: the first NST steps in flight; all but the last landed.
@@ -427,12 +575,12 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   // past the end the ring loads zeros and the last fragment read is
   // discarded.
   //
-  // vmcnt retires loads in order but counts stores too, so a load wait issued
+  // vmcnt retires loads and stores in issue order, so a plain load wait issued
   // while the epilogue's stores are in flight would also wait for them.
-  // Hence, before a tile's epilogue every ring load but the newest step's is
-  // drained (waitcnt_vm<LOADS>), and the first two steps of the next tile
-  // (whose data needs only those loads) skip the vmcnt wait: the stores get
-  // two steps to complete before the next load wait.  Requires NST >= 4.
+  // Before a tile's epilogue every ring load but the newest step's is drained
+  // (waitcnt_vm<LOADS>), so the first two steps of the next tile skip the
+  // wait, and the steps up to NST-2 use a count that also leaves the
+  // epilogue's stores in flight (wait kind 2 below).  Requires NST >= 4.
   static_assert(NST >= 4, "two wait-free steps need a 4-deep ring");
   constexpr int NMF = FN * FM;                   // MFMAs per step
   constexpr int NRD = 2 * (FN + FM);             // 16-byte LDS reads per step
@@ -440,10 +588,18 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   // reads over the first half and loads from the first MFMA or from the half.
   constexpr int RDU = NMF * 3 / 4;  // MFMAs the fragment reads spread over
   constexpr int LD0 = NMF / 4;      // first MFMA followed by a ring load
-  auto step = [&](Frags& cur, Frags& nxt, int64_t s, int kt, bool wait)
+  // Wait kinds: 0 none, 1 the step's loads (the NST-2 newer steps' loads may
+  // be in flight), 2 the same with the previous tile's staged stores also
+  // allowed in flight (they were issued after the loads waited for).
+
+  constexpr bool kCanAdjust = OUT != FR_DTYPE_FP32 && (NST - 2) * LOADS + kStagedStores <= 63;
+  auto step = [&](Frags& cur, Frags& nxt, int64_t s, int kt, int wait)
       __attribute__((always_inline)) {
     __builtin_amdgcn_sched_barrier(0);
-    if (wait) waitcnt_vm<(NST - 2) * LOADS>();
+    if (kCanAdjust && wait == 2)
+      waitcnt_vm<kCanAdjust ? (NST - 2) * LOADS + kStagedStores : 0>();
+    else if (wait != 0)
+      waitcnt_vm<(NST - 2) * LOADS>();
     lds_barrier();
     const int lk0 = kt + NST;
     const int lk = lk0 < KT ? lk0 : lk0 - KT;
@@ -478,17 +634,23 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
       __builtin_amdgcn_sched_barrier(0);
     }
   };
+  // A step's slot was loaded NST-1 steps earlier; for steps 2 .. NST-2 of a
+  // tile that lies before the previous tile's epilogue, whose stores then sit
+  // between those loads and the newest ones in the vmcnt order.  After a
+  // staged epilogue (a known store count) those steps allow the stores in
+  // flight; after any other (or none) they wait for them.
   int64_t s = 0;
+  bool staged_prev = false;
   for (int64_t tile = 0; tile < my_tiles; ++tile) {
-    step(f0, f1, s, 0, false);
-    step(f1, f0, s + 1, 1, false);
+    step(f0, f1, s, 0, 0);
+    step(f1, f0, s + 1, 1, 0);
     s += 2;
     for (int kt = 2; kt < KT; kt += 2, s += 2) {  // KT is even
-      step(f0, f1, s, kt, true);
-      step(f1, f0, s + 1, kt + 1, true);
+      step(f0, f1, s, kt, staged_prev && kt <= NST - 2 ? 2 : 1);
+      step(f1, f0, s + 1, kt + 1, staged_prev && kt + 1 <= NST - 2 ? 2 : 1);
     }
     waitcnt_vm<LOADS>();
-    epilogue(tile);
+    staged_prev = epilogue(tile);
     zero_acc();
     load_scales(tile + 1);
     bb_cur = bb_nxt;
