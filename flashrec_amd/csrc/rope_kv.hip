@@ -84,7 +84,7 @@ __global__ __launch_bounds__(256) void qk_rope_kv_d128(RopeArgs a) {
     u32x4 xv[R];
 #pragma unroll
     for (int r = 0; r < R; ++r)
-      xv[r] = *reinterpret_cast<const u32x4*>(a.v + t * a.svt + (h0 + 4 * r) * a.svh + e0);
+      xv[r] = ldnt(reinterpret_cast<const u32x4*>(a.v + t * a.svt + (h0 + 4 * r) * a.svh + e0));
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       float x[8];
@@ -92,7 +92,7 @@ __global__ __launch_bounds__(256) void qk_rope_kv_d128(RopeArgs a) {
       u32x2 o;
       o[0] = e4m3x4_torch(x[0], x[1], x[2], x[3]);
       o[1] = e4m3x4_torch(x[4], x[5], x[6], x[7]);
-      *reinterpret_cast<u32x2*>(a.vc + slot * a.scvp + (h0 + 4 * r) * a.scvh + e0) = o;
+      stnt(reinterpret_cast<u32x2*>(a.vc + slot * a.scvp + (h0 + 4 * r) * a.scvh + e0), o);
     }
     return;
   }
@@ -105,7 +105,7 @@ __global__ __launch_bounds__(256) void qk_rope_kv_d128(RopeArgs a) {
 
   u32x4 xv[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) xv[r] = *reinterpret_cast<const u32x4*>(src + 4 * r * hstride + e0);
+  for (int r = 0; r < R; ++r) xv[r] = ldnt(reinterpret_cast<const u32x4*>(src + 4 * r * hstride + e0));
   u32x4 wv;
   if (FUSED) wv = *reinterpret_cast<const u32x4*>(wp + e0);
   if (pos < 0 || pos >= a.cs_rows) return;  // no cache row: leave q / slot untouched
@@ -162,14 +162,14 @@ __global__ __launch_bounds__(256) void qk_rope_kv_d128(RopeArgs a) {
     if (is_q || !FUSED) {
       const u32x4 o = yb;
       uint16_t* dst = is_q ? a.q + t * a.sqt + h * a.sqh : const_cast<uint16_t*>(a.k + t * a.skt + h * a.skh);
-      *reinterpret_cast<u32x4*>(dst + e0) = o;
+      stnt(reinterpret_cast<u32x4*>(dst + e0), o);
     } else if (slot_ok) {
       float y[8];
       unpack8(yb, y);
       u32x2 o;
       o[0] = e4m3x4_torch(y[0], y[1], y[2], y[3]);
       o[1] = e4m3x4_torch(y[4], y[5], y[6], y[7]);
-      *reinterpret_cast<u32x2*>(a.kc + slot * a.sckp + h * a.sckh + e0) = o;
+      stnt(reinterpret_cast<u32x2*>(a.kc + slot * a.sckp + h * a.sckh + e0), o);
     }
   }
 }

@@ -212,8 +212,8 @@ __global__ __launch_bounds__(256) void row_kernel_vec(RowArgs a) {
     u32x4 p[NV], uv[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-      p[j] = in(j) ? *reinterpret_cast<const u32x4*>(xr + col(j)) : u32x4{0, 0, 0, 0};
-      uv[j] = in(j) ? *reinterpret_cast<const u32x4*>(xr + K + col(j)) : u32x4{0, 0, 0, 0};
+      p[j] = in(j) ? ldnt(reinterpret_cast<const u32x4*>(xr + col(j))) : u32x4{0, 0, 0, 0};
+      uv[j] = in(j) ? ldnt(reinterpret_cast<const u32x4*>(xr + K + col(j))) : u32x4{0, 0, 0, 0};
     }
     auto chunk = [&](int j) __attribute__((always_inline)) {
       float g[8], u[8];
@@ -243,7 +243,7 @@ __global__ __launch_bounds__(256) void row_kernel_vec(RowArgs a) {
       uint16_t* orow = reinterpret_cast<uint16_t*>(a.q) + row * a.ldq;
 #pragma unroll
       for (int j = 0; j < NV; ++j)
-        if (in(j)) *reinterpret_cast<u32x4*>(orow + col(j)) = p[j];
+        if (in(j)) stnt(reinterpret_cast<u32x4*>(orow + col(j)), p[j]);
       return;
     }
     uint32_t mb = 0;
@@ -266,7 +266,7 @@ __global__ __launch_bounds__(256) void row_kernel_vec(RowArgs a) {
         u32x2 o;
         o[0] = cvt_pk_e4m3<true>(t[2], t[3], cvt_pk_e4m3<false>(t[0], t[1], 0u));
         o[1] = cvt_pk_e4m3<true>(t[6], t[7], cvt_pk_e4m3<false>(t[4], t[5], 0u));
-        if (in(j)) *reinterpret_cast<u32x2*>(qrow + col(j)) = o;
+        if (in(j)) stnt(reinterpret_cast<u32x2*>(qrow + col(j)), o);
       }
     } else {
 #pragma unroll
@@ -278,7 +278,7 @@ __global__ __launch_bounds__(256) void row_kernel_vec(RowArgs a) {
         u32x2 o;
         o[0] = e4m3x4_clamped(t[0], t[1], t[2], t[3]);
         o[1] = e4m3x4_clamped(t[4], t[5], t[6], t[7]);
-        if (in(j)) *reinterpret_cast<u32x2*>(qrow + col(j)) = o;
+        if (in(j)) stnt(reinterpret_cast<u32x2*>(qrow + col(j)), o);
       }
     }
   };
@@ -296,9 +296,9 @@ __global__ __launch_bounds__(256) void row_kernel_vec(RowArgs a) {
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       if (in(j)) {
-        xv[j] = *reinterpret_cast<const u32x4*>(xr + col(j));
-        if (MODE == kSilu) uv[j] = *reinterpret_cast<const u32x4*>(xr + K + col(j));
-        if (MODE == kAddRms) uv[j] = *reinterpret_cast<const u32x4*>(a.res + row * a.ldr + col(j));
+        xv[j] = ldnt(reinterpret_cast<const u32x4*>(xr + col(j)));
+        if (MODE == kSilu) uv[j] = ldnt(reinterpret_cast<const u32x4*>(xr + K + col(j)));
+        if (MODE == kAddRms) uv[j] = ldnt(reinterpret_cast<const u32x4*>(a.res + row * a.ldr + col(j)));
       } else {
         xv[j] = u32x4{0, 0, 0, 0};
         uv[j] = u32x4{0, 0, 0, 0};
@@ -318,7 +318,7 @@ __global__ __launch_bounds__(256) void row_kernel_vec(RowArgs a) {
           v[j][2 * i] = __uint_as_float(o[i] << 16);
           v[j][2 * i + 1] = __uint_as_float(o[i] & 0xFFFF0000u);
         }
-        if (in(j)) *reinterpret_cast<u32x4*>(a.res + row * a.ldr + col(j)) = o;
+        if (in(j)) stnt(reinterpret_cast<u32x4*>(a.res + row * a.ldr + col(j)), o);
       }
     }
 
@@ -355,7 +355,7 @@ __global__ __launch_bounds__(256) void row_kernel_vec(RowArgs a) {
           u32x4 o;
 #pragma unroll
           for (int i = 0; i < 4; ++i) o[i] = pack_bf16x2(v[j][2 * i], v[j][2 * i + 1]);
-          *reinterpret_cast<u32x4*>(orow + col(j)) = o;
+          stnt(reinterpret_cast<u32x4*>(orow + col(j)), o);
         }
       }
       continue;
@@ -384,7 +384,7 @@ __global__ __launch_bounds__(256) void row_kernel_vec(RowArgs a) {
         u32x2 o;
         o[0] = cvt_pk_e4m3<true>(t[2], t[3], cvt_pk_e4m3<false>(t[0], t[1], 0u));
         o[1] = cvt_pk_e4m3<true>(t[6], t[7], cvt_pk_e4m3<false>(t[4], t[5], 0u));
-        if (in(j)) *reinterpret_cast<u32x2*>(qrow + col(j)) = o;
+        if (in(j)) stnt(reinterpret_cast<u32x2*>(qrow + col(j)), o);
       }
     } else {
       // NaN or inf in the row: plain IEEE division and torch's NaN codes.
@@ -396,7 +396,7 @@ __global__ __launch_bounds__(256) void row_kernel_vec(RowArgs a) {
         u32x2 o;
         o[0] = e4m3x4_clamped(t[0], t[1], t[2], t[3]);
         o[1] = e4m3x4_clamped(t[4], t[5], t[6], t[7]);
-        if (in(j)) *reinterpret_cast<u32x2*>(qrow + col(j)) = o;
+        if (in(j)) stnt(reinterpret_cast<u32x2*>(qrow + col(j)), o);
       }
     }
   }
