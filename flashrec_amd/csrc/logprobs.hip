@@ -2,8 +2,13 @@
 // Replaces the `F.log_softmax(logits.float(), dim=-1)` of
 // python/flashrec/logits.py:118-120 and :136-137.
 //
-// One wave64 per row, two passes: an online (max, sum of exp) pass, then
-// out = x - max - log(sum).  In place is allowed (out == x).
+// Rows of N = 1024 * NCH (the SID head: 8192): one 256-thread workgroup per
+// row holds the row in registers (NCH float4 per thread, read once with
+// streaming loads), reduces max and sum of exp over the workgroup, and
+// writes x - max - log(sum) once: HBM-bound, 8 bytes per element.
+// Other widths: one wave64 per row, an online (max, sum of exp) pass, then a
+// second read for the output.  In place is allowed (out == x).  A NaN in a
+// row, or a row of -inf, gives NaN everywhere, as torch's log_softmax.
 #include "fr_common.h"
 
 namespace fr {
@@ -39,6 +44,41 @@ __global__ __launch_bounds__(256) void log_softmax_rows(const float* x, int64_t 
   for (int64_t e = lane; e < N; e += 64) orow[e] = xr[e] - lse;
 }
 
+template <int NCH>
+__global__ __launch_bounds__(256) void log_softmax_rows_block(const float* x, int64_t ldx, float* out,
+                                                              int64_t ldo) {
+  __shared__ float red[8];
+  const int t = threadIdx.x;
+  const int lane = t & 63, w = t >> 6;
+  const int64_t row = blockIdx.x;
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const f32x4* xr = reinterpret_cast<const f32x4*>(x + row * ldx);
+  f32x4 v[NCH];
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) v[j] = ldnt(xr + t + 256 * j);
+  // max; a NaN anywhere makes the row NaN below (x - max is NaN for it, and
+  // the sum of exp with it)
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int j = 0; j < NCH; ++j)
+    m = __builtin_fmaxf(__builtin_fmaxf(m, __builtin_fmaxf(v[j].x, v[j].y)), __builtin_fmaxf(v[j].z, v[j].w));
+  m = wave_max(m);
+  if (lane == 0) red[w] = m;
+  __syncthreads();
+  m = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) s += (expf(v[j].x - m) + expf(v[j].y - m)) + (expf(v[j].z - m) + expf(v[j].w - m));
+  s = wave_sum(s);
+  if (lane == 0) red[4 + w] = s;
+  __syncthreads();
+  s = (red[4] + red[5]) + (red[6] + red[7]);
+  const float lse = m + logf(s);
+  f32x4* orow = reinterpret_cast<f32x4*>(out + row * ldo);
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) stnt(orow + t + 256 * j, v[j] - lse);
+}
+
 }  // namespace fr
 
 extern "C" int fr_log_softmax_f32(const float* x, int64_t ldx, float* out, int64_t ldo, int64_t M,
@@ -46,6 +86,19 @@ extern "C" int fr_log_softmax_f32(const float* x, int64_t ldx, float* out, int64
   if (M < 0 || N < 0) return FR_EINVAL;
   if (M == 0 || N == 0) return FR_OK;
   if (!x || !out || ldx < N || ldo < N) return FR_EINVAL;
+  const bool aligned = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out)) & 15) == 0 &&
+                       (ldx & 3) == 0 && (ldo & 3) == 0 && M <= 0x7FFFFFFF;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (aligned && N == 8192) {
+    hipLaunchKernelGGL(fr::log_softmax_rows_block<8>, dim3(static_cast<unsigned>(M)), dim3(256), 0, st, x, ldx,
+                       out, ldo);
+    return hipGetLastError() == hipSuccess ? FR_OK : FR_ELAUNCH;
+  }
+  if (aligned && N == 4096) {
+    hipLaunchKernelGGL(fr::log_softmax_rows_block<4>, dim3(static_cast<unsigned>(M)), dim3(256), 0, st, x, ldx,
+                       out, ldo);
+    return hipGetLastError() == hipSuccess ? FR_OK : FR_ELAUNCH;
+  }
   hipLaunchKernelGGL(fr::log_softmax_rows, dim3(static_cast<unsigned>((M + 3) / 4)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), x, ldx, out, ldo, M, N);
   return hipGetLastError() == hipSuccess ? FR_OK : FR_ELAUNCH;
