@@ -401,9 +401,10 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   // instructions; measured in one process against the staged form, they were
   // 1-12 % slower on every tile shape, so they are off.
   constexpr bool kDirectStores = false;
-  constexpr int kStagedStores = kDirectStores ? 4 * FN * FM : 2 * FN * FM;  // stores per wave per tile
-  // Returns whether the bf16/fp16 fast path ran (and so issued exactly
-  // kStagedStores stores per wave).
+  // stores per wave per tile on the fast paths (fp32: 16 bytes per (i, j, q))
+  constexpr int kStagedStores = (OUT == FR_DTYPE_FP32 || kDirectStores) ? 4 * FN * FM : 2 * FN * FM;
+  // Returns whether a fast path ran (and so issued exactly kStagedStores
+  // stores per wave).
   auto epilogue = [&](int64_t local) -> bool __attribute__((always_inline)) {
     int64_t tm, tn;
     tile_coords(blockIdx.x + local * G, nt, tilesM, tm, tn);
@@ -463,7 +464,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
           }
         }
       }
-      return false;
+      return true;
     }
     // bf16 / fp16: per pass (j, two column blocks) the converted outputs go
     // to a 32 x 128-byte staging tile (16-byte chunk c of row r at slot
@@ -592,12 +593,15 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   // be in flight), 2 the same with the previous tile's staged stores also
   // allowed in flight (they were issued after the loads waited for).
 
-  constexpr bool kCanAdjust = OUT != FR_DTYPE_FP32 && (NST - 2) * LOADS + kStagedStores <= 63;
+  // The count is capped at vmcnt's 63: a smaller count only waits for the
+  // oldest few stores as well (conservative).
+  constexpr int kAdjN = (NST - 2) * LOADS + kStagedStores < 63 ? (NST - 2) * LOADS + kStagedStores : 63;
+  constexpr bool kCanAdjust = true;
   auto step = [&](Frags& cur, Frags& nxt, int64_t s, int kt, int wait)
       __attribute__((always_inline)) {
     __builtin_amdgcn_sched_barrier(0);
     if (kCanAdjust && wait == 2)
-      waitcnt_vm<kCanAdjust ? (NST - 2) * LOADS + kStagedStores : 0>();
+      waitcnt_vm<kAdjN>();
     else if (wait != 0)
       waitcnt_vm<(NST - 2) * LOADS>();
     lds_barrier();
