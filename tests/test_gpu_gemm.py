@@ -125,3 +125,20 @@ def test_gemm_config1_full_size_rows(dev):
     lit = ops.fp8_scaled_mm_torch_cpu(qa[rows], qw.t(), sa[rows], sw, torch.bfloat16)
     assert max_abs_rel(got, lit.float()) < TOL
     assert torch.isfinite(out).all()
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32, torch.float16])
+@pytest.mark.parametrize("m,n,k", [(4096 + 100, 12288, 2048), (4096, 2048 + 64, 6144)])
+def test_gemm_multi_tile_edges(dev, m, n, k, out_dtype):
+    """Several tiles per workgroup with edge tiles among them: after a
+    partial tile's epilogue the next tile's first waits must not assume the
+    full tile's store count (and after a full one they may).  Seeded rows,
+    including every row of the last (partial) m-tile, against the oracle."""
+    qa, sa, qw, sw = _operands(m, n, k, seed=m + n)
+    out = _run(dev, qa, sa, qw, sw, out_dtype=out_dtype).cpu()
+    g = torch.Generator().manual_seed(5)
+    rows = torch.cat([torch.randperm(m, generator=g)[:48], torch.arange(m - 40, m)])
+    ref = ops.fp8_scaled_mm(qa[rows], qw.t(), sa[rows], sw)
+    got = out[rows].float()
+    assert max_abs_rel(got, ref) < TOL
+    assert torch.isfinite(out).all()
