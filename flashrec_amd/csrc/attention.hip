@@ -256,7 +256,7 @@ __device__ __forceinline__ bool group_shares_block(const AttnArgs& a, int64_t t0
 // The keys past the shared prefix run through the same block with each
 // token's own keys (NREP per token per block) and every query masked to its
 // own token's keys.  A shared 128-slot prefix is thus read and multiplied
-// once for all 32 queries (config-4 decode: 57 us a layer for 4096 beams,
+// once for all 32 queries (config-4 decode: 44 us a layer for 4096 beams,
 // against 189 us token by token).
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -276,7 +276,7 @@ __device__ __forceinline__ bf16x8_t e4m3x8_to_bf16(uint32_t w0, uint32_t w1) {
 constexpr int kVRow = 288;  // LDS bytes per staged V row: 256 + 32 (bank spread)
 
 template <int NREP>
-__global__ __launch_bounds__(256) void paged_attn_grouped_d128(AttnArgs a) {
+__global__ __launch_bounds__(256, 2) void paged_attn_grouped_d128(AttnArgs a) {
   constexpr int TOK = 32 / NREP;  // tokens per group
   __shared__ __attribute__((aligned(16))) uint8_t lds[4 * 32 * kVRow];
   const int lane = threadIdx.x & 63;
@@ -484,29 +484,19 @@ __global__ __launch_bounds__(256) void paged_attn_grouped_d128(AttnArgs a) {
     }
   };
 
-  // two blocks in flight: block b + 1's gathers are issued before block b
-  // is computed
-  Loaded LA, LB;
-  if (nblocks > 0) load(0, LA);
+  // One block's gathers at a time: holding a second block's gathers in
+  // registers (as a prefetch) needs 329 registers and one wave per SIMD;
+  // without it the kernel fits two waves per SIMD (launch bound below), and
+  // the other wave hides the gather latency (config-4 decode 62 -> 44 us).
+  Loaded LA;
   int32_t bi = 0;
-  for (; bi + 1 < nshared; bi += 2) {
-    load(bi + 1, LB);
+  for (; bi < nshared; ++bi) {
+    load(bi, LA);
     compute(bi, LA, std::false_type{});
-    load(bi + 2, LA);
-    compute(bi + 1, LB, std::false_type{});
   }
-  if (bi < nshared) {
-    load(bi + 1, LB);
-    compute(bi, LA, std::false_type{});
-    LA = LB;
-    ++bi;
-  }
-  for (; bi < nblocks; bi += 2) {
-    load(bi + 1, LB);
+  for (; bi < nblocks; ++bi) {
+    load(bi, LA);
     compute(bi, LA, std::true_type{});
-    if (bi + 1 >= nblocks) break;
-    load(bi + 2, LA);
-    compute(bi + 1, LB, std::true_type{});
   }
 
   // ---- normalise and store this lane's query (64 of its 128 dims)
