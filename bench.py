@@ -148,7 +148,8 @@ def _decode_step_case(dev):
     k0, v0 = m.pool.k[0], m.pool.v[0]
 
     def step(_i):
-        paged_attention(q, k0, v0, p["indices"], p["start"], p["len"], shape.head_dim ** -0.5, out=o)
+        paged_attention(q, k0, v0, p["indices"], p["start"], p["len"], shape.head_dim ** -0.5, out=o,
+                        group_prefix=p["group_prefix"])
 
     ms_a = _graph_timed(step, 1)
     flops = 4.0 * rows * shape.q_heads * m.seq_len * shape.head_dim

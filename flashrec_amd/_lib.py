@@ -66,8 +66,10 @@ SIGNATURES = {
     "fr_paged_attention_fp8": [
         _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,  # q, k_cache, v_cache + strides
         _I64, _P, _P, _P,  # num_slots, kv_indices, kv_start, kv_len
-        _P, _I64, _I64, _I64, _I64, _I64, _I64, _F32, _P,  # out + strides, T, Hq, Hk, D, scale, stream
+        _P, _I64, _I64, _I64, _I64, _I64, _I64, _F32, _P, _P,  # out + strides, T, Hq, Hk, D, scale, plan, stream
     ],
+    "fr_paged_attention_plan_size": [_I64, _I64, _I64],
+    "fr_paged_attention_plan": [_P, _P, _P, _I64, _I64, _I64, _P, _P],
 }
 
 _LIB: Optional[ctypes.CDLL] = None
@@ -99,6 +101,7 @@ def load() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.argtypes = argtypes
         fn.restype = ctypes.c_int
+    lib.fr_paged_attention_plan_size.restype = ctypes.c_int64
     _LIB = lib
     return lib
 

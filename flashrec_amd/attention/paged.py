@@ -17,7 +17,7 @@ from typing import Dict, List, Optional
 
 import torch
 
-from flashrec_amd._lib import call, require_device, stream_of
+from flashrec_amd._lib import call, load, require_device, stream_of
 
 
 class AttentionBackend:
@@ -68,6 +68,8 @@ class AttentionBackend:
                 "indices": torch.zeros(bs * max_seq_len, dtype=torch.int32, device=dev),
                 "last": torch.ones(bs, dtype=torch.int32, device=dev),
                 "kv_len": torch.zeros(bs, dtype=torch.int32, device=dev),
+                "group_prefix": torch.zeros(max(plan_size(bs, self.num_qo_heads, self.num_kv_heads), 1),
+                                            dtype=torch.int32, device=dev),
             }
 
     def graph_bufs(self, bs: int) -> Optional[dict]:
@@ -83,7 +85,9 @@ class AttentionBackend:
 
     # ----------------------------------------------------------------- plan
     def prepare(self, batch) -> None:
-        """Per-token slot ranges for every layer of this batch (flashinfer.py:201-210)."""
+        """Per-token slot ranges for every layer of this batch (flashinfer.py:201-210),
+        and the shared-prefix plan of its query groups (one kernel, reused by
+        every layer's attention)."""
         if batch.kv_indices is None:
             self._plan = None
             return
@@ -91,6 +95,14 @@ class AttentionBackend:
             self._plan = self._plan_prefill(batch)
         else:
             self._plan = self._plan_decode(batch)
+        n = int(self._plan["start"].numel())
+        bufs = self._graph_bufs.get(self._graph_bs) if self._graph_bs is not None else None
+        gp = None
+        if bufs is not None and not batch.is_prefill:
+            gp = bufs["group_prefix"][: max(plan_size(n, self.num_qo_heads, self.num_kv_heads), 1)]
+        self._plan["group_prefix"] = attention_plan(self._plan["indices"], self._plan["start"],
+                                                    self._plan["len"], self.num_qo_heads,
+                                                    self.num_kv_heads, out=gp)
 
     def _plan_decode(self, batch) -> Dict[str, torch.Tensor]:
         n = int(batch.n_rows)
@@ -148,16 +160,44 @@ class AttentionBackend:
             raise RuntimeError("AttentionBackend.forward before prepare() (kv_indices required)")
         return paged_attention(q, self.kv_pool.k_cache(layer_id), self.kv_pool.v_cache(layer_id),
                                self._plan["indices"], self._plan["start"], self._plan["len"],
-                               self.scale)
+                               self.scale, group_prefix=self._plan.get("group_prefix"))
+
+
+def plan_size(T: int, hq: int, hk: int) -> int:
+    """Entries of an attention plan for T query tokens (groups of 32 / (hq / hk))."""
+    n = int(load().fr_paged_attention_plan_size(int(T), int(hq), int(hk)))
+    if n < 0:
+        raise ValueError(f"unsupported head ratio {hq}/{hk}")
+    return n
+
+
+def attention_plan(kv_indices: torch.Tensor, kv_start: torch.Tensor, kv_len: torch.Tensor,
+                   hq: int, hk: int, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The shared slot prefix (rounded down to 32) of each group of 32 / (hq /
+    hk) consecutive query tokens: computed once per batch, passed to every
+    layer's ``paged_attention`` as ``group_prefix``."""
+    require_device(kv_indices, kv_start, kv_len)
+    T = int(kv_start.numel())
+    n = plan_size(T, hq, hk)
+    if out is None:
+        out = torch.empty(max(n, 1), dtype=torch.int32, device=kv_start.device)
+    if out.dtype != torch.int32 or not out.is_contiguous() or out.numel() < n:
+        raise ValueError("plan buffer must be contiguous int32 with plan_size entries")
+    call("fr_paged_attention_plan", kv_indices.data_ptr(), kv_start.data_ptr(), kv_len.data_ptr(),
+         T, int(hq), int(hk), out.data_ptr(), stream_of(kv_start))
+    return out
 
 
 def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                     kv_indices: torch.Tensor, kv_start: torch.Tensor, kv_len: torch.Tensor,
-                    scale: float, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                    scale: float, out: Optional[torch.Tensor] = None,
+                    group_prefix: Optional[torch.Tensor] = None) -> torch.Tensor:
     """softmax(q k^T * scale) v over each query token's slot list.
 
     q: [T, Hq, 128] bf16 (unit inner stride); k_cache / v_cache: [slots, Hk,
     128] float8_e4m3fn; kv_indices / kv_start / kv_len: int32 on the device.
+    group_prefix: the plan of ``attention_plan`` for the same slot lists, or
+    None (each call then finds the shared prefixes itself).
     """
     require_device(q, k_cache, v_cache, kv_indices, kv_start, kv_len)
     if q.dtype != torch.bfloat16:
@@ -183,5 +223,5 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
          v_cache.data_ptr(), v_cache.stride(0), v_cache.stride(1),
          slots, kv_indices.data_ptr(), kv_start.data_ptr(), kv_len.data_ptr(),
          out.data_ptr(), out.stride(0), out.stride(1),
-         T, Hq, Hk, D, float(scale), stream_of(q))
+         T, Hq, Hk, D, float(scale), 0 if group_prefix is None else group_prefix.data_ptr(), stream_of(q))
     return out

@@ -39,6 +39,7 @@ struct AttnArgs {
   int64_t sot, soh;
   int64_t T, Hq, Hk, num_slots;
   float qscale;  // softmax scale * log2(e)
+  const int32_t* gp;  // [groups] shared prefix rounded down to 32 (0: none), or null
 };
 
 // Sum over the 8 lanes of each aligned group of 8 (DPP: half-row mirror,
@@ -235,6 +236,57 @@ __device__ __forceinline__ bool group_shares_block(const AttnArgs& a, int64_t t0
   return __ballot(!ok) == 0;
 }
 
+// Longest slot prefix shared by every token of the group starting at t0,
+// rounded down to a multiple of 32 (0 when the tokens do not share 32
+// slots).  Lanes 0 .. TOK-1 fetch the tokens' (start, length) in one load;
+// every comparison load of a 64-position chunk is issued before any is used.
+template <int TOK>
+__device__ __forceinline__ int32_t group_prefix32(const AttnArgs& a, int64_t t0, int lane) {
+  const int ntok = static_cast<int>(min<int64_t>(TOK, a.T - t0));
+  int32_t my_start = 0, my_len = 0x7FFFFFFF;
+  if (lane < ntok) {
+    my_start = a.kv_start[t0 + lane];
+    my_len = a.kv_len[t0 + lane];
+  }
+  int32_t lenmin = my_len;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) lenmin = min(lenmin, __shfl_xor(lenmin, o, 64));
+  int32_t starts[TOK];
+#pragma unroll
+  for (int tt = 0; tt < TOK; ++tt) starts[tt] = __builtin_amdgcn_readlane(my_start, tt);
+  const int32_t* i0 = a.kv_indices + starts[0];
+  int32_t P = 0;
+  for (int32_t c = 0; c < lenmin; c += 64) {
+    const int32_t pos = c + lane;
+    const bool in = pos < lenmin;
+    const int32_t s0 = in ? i0[pos] : 0;
+    int32_t sv[TOK];
+#pragma unroll
+    for (int tt = 1; tt < TOK; ++tt) sv[tt] = (in && tt < ntok) ? a.kv_indices[starts[tt] + pos] : s0;
+    bool ok = in;
+#pragma unroll
+    for (int tt = 1; tt < TOK; ++tt) ok = ok && sv[tt] == s0;
+    const uint64_t bad = __ballot(!ok);
+    if (bad) {
+      P = c + __builtin_ctzll(bad);
+      break;
+    }
+    P = c + 64;
+  }
+  P = min(P, lenmin);
+  return P & ~31;
+}
+
+// The plan: one wave per group, the group's shared prefix for every layer.
+template <int TOK>
+__global__ __launch_bounds__(256) void attn_group_plan(AttnArgs a, int32_t* gp, int64_t groups) {
+  const int lane = threadIdx.x & 63;
+  const int64_t group = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (group >= groups) return;
+  const int32_t p = group_prefix32<TOK>(a, group * TOK, lane);
+  if (lane == 0) gp[group] = p;
+}
+
 // ---------------------------------------------------------------------------
 // Grouped kernel (the default): one wave per (group of 32 / NREP consecutive
 // query tokens, kv head), i.e. 32 query rows, on bf16 MFMA.
@@ -287,7 +339,7 @@ __global__ __launch_bounds__(256, 2) void paged_attn_grouped_d128(AttnArgs a) {
   const int64_t t0 = group * TOK;
   if (t0 >= a.T) return;
   // groups without a shared 32-slot block go to paged_attn_tokens_d128
-  if (!group_shares_block<TOK>(a, t0, lane)) return;
+  if (a.gp ? a.gp[group] == 0 : !group_shares_block<TOK>(a, t0, lane)) return;
   uint8_t* vs = lds + wave * (32 * kVRow);
   const int n = lane & 31;  // query column (and key row when loading)
   const int h = lane >> 5;  // half: dims 64h .. 64h + 63
@@ -304,42 +356,9 @@ __global__ __launch_bounds__(256, 2) void paged_attn_grouped_d128(AttnArgs a) {
       qb[s] = qok ? *reinterpret_cast<const u32x4*>(qp + 8 * s) : u32x4{0, 0, 0, 0};
   }
 
-  // ---- shared slot prefix of the group's tokens.  Lanes 0 .. TOK-1 fetch
-  // the tokens' (start, length) in one load; every comparison load of a
-  // 64-position chunk is issued before any is used.
-  const int ntok = static_cast<int>(min<int64_t>(TOK, a.T - t0));
-  int32_t my_start = 0, my_len = 0x7FFFFFFF;
-  if (lane < ntok) {
-    my_start = a.kv_start[t0 + lane];
-    my_len = a.kv_len[t0 + lane];
-  }
-  int32_t lenmin = my_len;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) lenmin = min(lenmin, __shfl_xor(lenmin, o, 64));
-  int32_t starts[TOK];
-#pragma unroll
-  for (int tt = 0; tt < TOK; ++tt) starts[tt] = __builtin_amdgcn_readlane(my_start, tt);
-  const int32_t* i0 = a.kv_indices + starts[0];
-  int32_t P = 0;
-  for (int32_t c = 0; c < lenmin; c += 64) {
-    const int32_t pos = c + lane;
-    const bool in = pos < lenmin;
-    const int32_t s0 = in ? i0[pos] : 0;
-    int32_t sv[TOK];
-#pragma unroll
-    for (int tt = 1; tt < TOK; ++tt) sv[tt] = (in && tt < ntok) ? a.kv_indices[starts[tt] + pos] : s0;
-    bool ok = in;
-#pragma unroll
-    for (int tt = 1; tt < TOK; ++tt) ok = ok && sv[tt] == s0;
-    const uint64_t bad = __ballot(!ok);
-    if (bad) {
-      P = c + __builtin_ctzll(bad);
-      break;
-    }
-    P = c + 64;
-  }
-  P = min(P, lenmin);
-  const int32_t P32 = P & ~31;
+  // ---- shared slot prefix of the group's tokens: from the plan, or found here
+  const int32_t P32 = a.gp ? a.gp[group] : group_prefix32<TOK>(a, t0, lane);
+  const int32_t* i0 = a.kv_indices + a.kv_start[t0];
 
   // ---- running softmax state of this lane's query (the two halves hold the
   // same m; l and O are per half: O^T rows 32mt + 8(v/4) + 4h + v%4)
@@ -528,7 +547,8 @@ __global__ __launch_bounds__(64 * token_waves<NREP>()) void paged_attn_tokens_d1
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * TOK;
-  if (t0 >= a.T || group_shares_block<TOK>(a, t0, lane)) return;
+  if (t0 >= a.T) return;
+  if (a.gp ? a.gp[blockIdx.x] != 0 : group_shares_block<TOK>(a, t0, lane)) return;
   const int ntok = static_cast<int>(min<int64_t>(TOK, a.T - t0));
   const int pairs = ntok * static_cast<int>(a.Hk);
   for (int p = wave; p < pairs; p += token_waves<NREP>())
@@ -556,7 +576,8 @@ extern "C" int fr_paged_attention_fp8(const void* q, int64_t sqt, int64_t sqh, c
                                       int64_t svh, int64_t num_slots, const int32_t* kv_indices,
                                       const int32_t* kv_start, const int32_t* kv_len, void* out,
                                       int64_t sot, int64_t soh, int64_t T, int64_t Hq, int64_t Hk,
-                                      int64_t D, float scale, void* stream) {
+                                      int64_t D, float scale, const int32_t* group_prefix,
+                                      void* stream) {
   if (T < 0 || Hq <= 0 || Hk <= 0 || D <= 0) return FR_EINVAL;
   if (T == 0) return FR_OK;
   if (!q || !k_cache || !v_cache || !kv_indices || !kv_start || !kv_len || !out) return FR_EINVAL;
@@ -587,6 +608,7 @@ extern "C" int fr_paged_attention_fp8(const void* q, int64_t sqt, int64_t sqh, c
   a.Hk = Hk;
   a.num_slots = num_slots;
   a.qscale = scale * 1.4426950408889634f;
+  a.gp = group_prefix;
   hipError_t e;
   switch (Hq / Hk) {
     case 1: e = launch_grouped<1>(a, static_cast<hipStream_t>(stream)); break;
@@ -596,4 +618,37 @@ extern "C" int fr_paged_attention_fp8(const void* q, int64_t sqt, int64_t sqh, c
     default: return FR_EUNSUPPORTED;
   }
   return e == hipSuccess ? FR_OK : FR_ELAUNCH;
+}
+
+extern "C" int64_t fr_paged_attention_plan_size(int64_t T, int64_t Hq, int64_t Hk) {
+  if (T < 0 || Hq <= 0 || Hk <= 0 || Hq % Hk != 0) return -1;
+  const int64_t nrep = Hq / Hk;
+  if (nrep != 1 && nrep != 2 && nrep != 4 && nrep != 8) return -1;
+  const int64_t tok = 32 / nrep;
+  return (T + tok - 1) / tok;
+}
+
+extern "C" int fr_paged_attention_plan(const int32_t* kv_indices, const int32_t* kv_start,
+                                       const int32_t* kv_len, int64_t T, int64_t Hq, int64_t Hk,
+                                       int32_t* group_prefix, void* stream) {
+  const int64_t groups = fr_paged_attention_plan_size(T, Hq, Hk);
+  if (groups < 0) return FR_EUNSUPPORTED;
+  if (groups == 0) return FR_OK;
+  if (!kv_indices || !kv_start || !kv_len || !group_prefix) return FR_EINVAL;
+  AttnArgs a{};
+  a.kv_indices = kv_indices;
+  a.kv_start = kv_start;
+  a.kv_len = kv_len;
+  a.T = T;
+  a.Hq = Hq;
+  a.Hk = Hk;
+  const dim3 grid(static_cast<unsigned>((groups + 3) / 4)), block(256);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (Hq / Hk) {
+    case 1: hipLaunchKernelGGL((attn_group_plan<32>), grid, block, 0, st, a, group_prefix, groups); break;
+    case 2: hipLaunchKernelGGL((attn_group_plan<16>), grid, block, 0, st, a, group_prefix, groups); break;
+    case 4: hipLaunchKernelGGL((attn_group_plan<8>), grid, block, 0, st, a, group_prefix, groups); break;
+    default: hipLaunchKernelGGL((attn_group_plan<4>), grid, block, 0, st, a, group_prefix, groups); break;
+  }
+  return hipGetLastError() == hipSuccess ? FR_OK : FR_ELAUNCH;
 }

@@ -136,7 +136,20 @@ int fr_paged_attention_fp8(const void* q, int64_t sqt, int64_t sqh, const void* 
                            int64_t skp, int64_t skh, const void* v_cache, int64_t svp, int64_t svh,
                            int64_t num_slots, const int32_t* kv_indices, const int32_t* kv_start,
                            const int32_t* kv_len, void* out, int64_t sot, int64_t soh, int64_t T,
-                           int64_t Hq, int64_t Hk, int64_t D, float scale, void* stream);
+                           int64_t Hq, int64_t Hk, int64_t D, float scale,
+                           const int32_t* group_prefix, void* stream);
+
+/* The per-batch attention plan, computed once for all layers that attend
+ * over the same kv_indices / kv_start / kv_len: for each group of 32 / (Hq /
+ * Hk) consecutive query tokens, the slot prefix all of them share, rounded
+ * down to 32 (0: none).  fr_paged_attention_plan_size gives the entry count
+ * (-1 for an unsupported head ratio).  Passing the plan as group_prefix to
+ * fr_paged_attention_fp8 skips that detection in every call (null: each call
+ * detects it).  No counterpart in the reference: flashinfer plans its own
+ * decode batches (python/flashrec/attention/flashinfer.py:262-349). */
+int64_t fr_paged_attention_plan_size(int64_t T, int64_t Hq, int64_t Hk);
+int fr_paged_attention_plan(const int32_t* kv_indices, const int32_t* kv_start, const int32_t* kv_len,
+                            int64_t T, int64_t Hq, int64_t Hk, int32_t* group_prefix, void* stream);
 
 /* Scratch bytes fr_genrec_mask_topk_expand needs for N requests of BW beams
  * and K picks (-1 when K is outside 1..1024).  No counterpart in the

@@ -15,13 +15,13 @@ HEADER = ROOT / "include" / "flashrec_amd.h"
 
 def _declared():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^int\s+(fr_\w+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^(?:int|int64_t)\s+(fr_\w+)\s*\(", text, flags=re.M)))
 
 
 def _declared_arity():
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
     out = {}
-    for name, args in re.findall(r"^int\s+(fr_\w+)\s*\(([^)]*)\)", text, flags=re.M | re.S):
+    for name, args in re.findall(r"^(?:int|int64_t)\s+(fr_\w+)\s*\(([^)]*)\)", text, flags=re.M | re.S):
         args = args.strip()
         out[name] = 0 if args in ("", "void") else len(args.split(","))
     return out

@@ -237,6 +237,22 @@ def test_grouped_prefixes_with_ragged_suffixes(dev, hq, hk):
     start[1:] = torch.cumsum(ln[:-1], 0)
     q = (torch.randn(len(lens), hq, 128, generator=g) * 2).to(torch.bfloat16)
     got = _run(dev, q, k, v, idx, start, ln)
+    # the once-per-batch plan gives the same prefixes as the in-call
+    # detection, hence the same bits
+    from flashrec_amd.attention import attention_plan, paged_attention
+
+    d = [t.to(dev) for t in (q, k, v, idx, start, ln)]
+    gp = attention_plan(d[3], d[4], d[5], hq, hk)
+    assert torch.equal(paged_attention(*d, SCALE, group_prefix=gp).cpu(), got.cpu())
+    expect = []
+    for g0 in range(0, len(rows), tok):
+        grp_rows = rows[g0: g0 + tok]
+        n = min(int(r.numel()) for r in grp_rows)
+        p = 0
+        while p < n and all(int(r[p]) == int(grp_rows[0][p]) for r in grp_rows):
+            p += 1
+        expect.append(32 * (p // 32))
+    assert gp.cpu()[: len(expect)].tolist() == expect
     # the oracle skips nothing: drop the out-of-pool slot from the expectation
     ref_rows = []
     keep_idx, keep_start, keep_len = [], [], []
