@@ -223,7 +223,8 @@ class Qwen3FP8DecodeStep:
             L.q_norm.eps, self.rotary.cos_sin_cache, self.pool.k[L.layer_id], self.pool.v[L.layer_id])
         if not stored:
             raise RuntimeError("fused QK-norm/RoPE/KV write rejected its inputs")
-        o = self.attn.forward(q.contiguous(), k, v, L.layer_id, self.batch, skip_store=True)
+        # q stays a strided view of qkv: the attention kernel takes row and head strides
+        o = self.attn.forward(q, k, v, L.layer_id, self.batch, skip_store=True)
         return L.o_proj(o.reshape(t, -1))
 
     def _layer(self, L: _Layer, x: torch.Tensor, residual: Optional[torch.Tensor]):
