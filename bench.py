@@ -167,6 +167,18 @@ def _bw_case(fn_factory, dev, nbytes, reps):
     return ms, nbytes / (ms * 1e-3) / 1e9
 
 
+def _copy_same_bytes(dev, nbytes, reps):
+    """A device-to-device copy moving the same bytes (nbytes/2 read, nbytes/2
+    written), timed and rotated like the case: what a launch of this size
+    reaches when it does nothing but stream."""
+    half = max(nbytes // 2, 1)
+    src = [torch.empty(half, dtype=torch.uint8, device=dev) for _ in range(reps)]
+    dst = [torch.empty_like(t) for t in src]
+    ms = _graph_timed(lambda i: dst[i].copy_(src[i]), reps)
+    del src, dst
+    return ms
+
+
 def _rms_case(dev, m, h, rotate):
     from flashrec_amd.kernel.rms_fp8 import rmsnorm_per_token_quant_fp8
 
@@ -374,11 +386,14 @@ def main() -> int:
         }
         result["extra_timing"] = ("GEMMs: HIP events around back-to-back launches; bandwidth kernels: "
                                   "one HIP-graph replay of 20 launches; inputs rotated over >512 MB "
-                                  "except the 3 MB config-0 case")
+                                  "except the 3 MB config-0 case; copy_ms_same_bytes: a device copy of the "
+                                  "same bytes timed the same way (the streaming limit at that size)")
         for name, (factory, nbytes, reps) in cases.items():
             msb, gbs = _bw_case(factory, dev, nbytes, reps)
             extra[name] = {"ms": round(msb, 5), "GB/s": round(gbs, 1),
                            "frac": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes}
+            torch.cuda.empty_cache()
+            extra[name]["copy_ms_same_bytes"] = round(_copy_same_bytes(dev, nbytes, reps), 5)
             torch.cuda.empty_cache()
         extra.update(_decode_step_case(dev))
         result["extra"] = extra
