@@ -352,18 +352,13 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     for (int r = 0; r < 2 * (FN + FM); ++r) read_one(f, slot, r);
   };
   v16f acc[FN][FM];
-  auto zero_acc = [&]() __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < FN; ++i)
-#pragma unroll
-      for (int j = 0; j < FM; ++j)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-  };
-  auto mfma_one = [&](Frags& f, int i, int j) __attribute__((always_inline)) {
+  // A tile's first K step starts its accumulators from the constant 0
+  // (the MFMA's inline-constant C operand) instead of clearing 256 AGPRs.
+  auto mfma_one = [&](Frags& f, int i, int j, bool first) __attribute__((always_inline)) {
     const v8i bv = (v8i)__builtin_shufflevector(breg(f, i, 0), breg(f, i, 1), 0, 1, 2, 3, 4, 5, 6, 7);
     const v8i av = (v8i)__builtin_shufflevector(f.a[j][0], f.a[j][1], 0, 1, 2, 3, 4, 5, 6, 7);
-    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, acc[i][j], 0, 0, 0, 0, 0, 0);
+    const v16f zero = {};
+    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, first ? zero : acc[i][j], 0, 0, 0, 0, 0, 0);
   };
 
   // ---- epilogue of one tile.  Lane l holds, per block (i, j), output row
@@ -411,18 +406,20 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     const int64_t m0 = tm * BM + wm * WM;
     const int64_t n0 = tn * BN + wn * WN;
     const bool fast = tm * BM + BM <= g.M && tn * BN + BN <= g.N && g.bias == nullptr &&
-                      (g.ldo * EB) % 16 == 0 && (reinterpret_cast<uintptr_t>(g.out) & 15) == 0;
+                      (g.ldo * EB) % 16 == 0 && (reinterpret_cast<uintptr_t>(g.out) & 15) == 0 &&
+                      g.ldo < (int64_t(1) << 22);  // tile offsets fit the 32-bit store offsets
     if (!fast) {
+      const int ls = lane_id_here();
 #pragma unroll
       for (int j = 0; j < FM; ++j) {
-        const int64_t m = m0 + j * 32 + (lane & 31);
+        const int64_t m = m0 + j * 32 + (ls & 31);
         if (m >= g.M) continue;
         const float sam = g.sa[m * g.sa_stride];
 #pragma unroll
         for (int i = 0; i < FN; ++i)
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const int64_t n = n0 + i * 32 + 8 * q + 4 * (lane >> 5);
+            const int64_t n = n0 + i * 32 + 8 * q + 4 * (ls >> 5);
             if (n >= g.N) continue;
             float v[4];
 #pragma unroll
@@ -433,6 +430,10 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
             store4<OUT>(g.out, g.ldo, m, n, g.N, v, g.bias);
           }
       }
+      // Retire this path's scale and bias loads here: the compiler's wait
+      // tracking otherwise carries them around the tile loop and makes the
+      // fast path wait for every load in flight before reusing a register.
+      waitcnt_vm<0>();
       return false;
     }
     // lane-derived values are formed here from a freshly computed lane id,
@@ -488,6 +489,16 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
         }
       }
     lds_wait_all(sb4, sam_r);
+    // Stores go through a buffer resource based at this wave's sub-tile: the
+    // lane's offset is formed once, each store's row/column step is a scalar
+    // offset (no 64-bit address arithmetic per store).
+    const uint64_t obase = reinterpret_cast<uint64_t>(static_cast<uint16_t*>(g.out) + m0 * g.ldo + n0);
+    const uint32_t olo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(obase));
+    const uint32_t ohi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(obase >> 32));
+    const __amdgpu_buffer_rsrc_t ro =
+        make_rsrc(reinterpret_cast<const void*>((static_cast<uint64_t>(ohi) << 32) | olo), 0xFFFFFFFFu);
+    const uint32_t ldo32 = static_cast<uint32_t>(g.ldo);
+    const uint32_t vo = ((lx >> 3) * ldo32 + (lx & 7) * 8) * 2;
     if constexpr (kDirectStores) {
       // stores straight from the accumulator layout: lane l writes the 4
       // outputs (8 bytes) of row l%32, columns 8q + 4(l/32) .. +3 of each block
@@ -540,10 +551,9 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
           u32x4 w[4];
           lds_read4_b128(ra[0], ra[1], ra[2], ra[3], w[0], w[1], w[2], w[3]);
   #pragma unroll
-          for (int rr = 0; rr < 4; ++rr) {
-            const int64_t off = (m0 + j * 32 + rr_row[rr]) * g.ldo + n0 + p * 64 + cg * 8;
-            *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(g.out) + off) = w[rr];
-          }
+          for (int rr = 0; rr < 4; ++rr)
+            __builtin_amdgcn_raw_buffer_store_b128(w[rr], ro, vo,
+                                                   static_cast<int>(((j * 32 + rr * 8) * ldo32 + p * 64) * 2), 0);
         }
       }
     }
@@ -561,7 +571,6 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   for (int st = 0; st < NST; ++st) issue(st, st < KT ? st : st - KT, st >= KT);
   waitcnt_vm<LOADS>();
   lds_barrier();
-  zero_acc();
   Frags f0, f1;
   read_frags(f0, 0);
 
@@ -597,7 +606,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   // oldest few stores as well (conservative).
   constexpr int kAdjN = (NST - 2) * LOADS + kStagedStores < 63 ? (NST - 2) * LOADS + kStagedStores : 63;
   constexpr bool kCanAdjust = true;
-  auto step = [&](Frags& cur, Frags& nxt, int64_t s, int kt, int wait)
+  auto step = [&](Frags& cur, Frags& nxt, int64_t s, int kt, int wait, bool first)
       __attribute__((always_inline)) {
     __builtin_amdgcn_sched_barrier(0);
     if (kCanAdjust && wait == 2)
@@ -627,7 +636,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
         for (int r = 0; r < NRD; ++r)
           if (r * RDU / NRD == u) read_one(nxt, nslot, r);
       }
-      mfma_one(cur, u / FM, u % FM);
+      mfma_one(cur, u / FM, u % FM, first);
       if (kOneB && u % FM == FM - 1) {
         read_one(nxt, nslot, 2 * (u / FM));
         read_one(nxt, nslot, 2 * (u / FM) + 1);
@@ -646,16 +655,15 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   int64_t s = 0;
   bool staged_prev = false;
   for (int64_t tile = 0; tile < my_tiles; ++tile) {
-    step(f0, f1, s, 0, 0);
-    step(f1, f0, s + 1, 1, 0);
+    step(f0, f1, s, 0, 0, true);
+    step(f1, f0, s + 1, 1, 0, false);
     s += 2;
     for (int kt = 2; kt < KT; kt += 2, s += 2) {  // KT is even
-      step(f0, f1, s, kt, staged_prev && kt <= NST - 2 ? 2 : 1);
-      step(f1, f0, s + 1, kt + 1, staged_prev && kt + 1 <= NST - 2 ? 2 : 1);
+      step(f0, f1, s, kt, staged_prev && kt <= NST - 2 ? 2 : 1, false);
+      step(f1, f0, s + 1, kt + 1, staged_prev && kt + 1 <= NST - 2 ? 2 : 1, false);
     }
     waitcnt_vm<LOADS>();
     staged_prev = epilogue(tile);
-    zero_acc();
     load_scales(tile + 1);
     bb_cur = bb_nxt;
     ba_cur = ba_nxt;
