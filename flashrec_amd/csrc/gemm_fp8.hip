@@ -392,12 +392,11 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   };
   // bf16/fp16 outputs leave the epilogue through an LDS staging tile as
   // 16-byte row segments.  8-byte stores straight from the accumulator
-  // layout (kDirectStores) need no LDS round trips but twice the store
-  // instructions; measured in one process against the staged form, they were
-  // 1-12 % slower on every tile shape, so they are off.
-  constexpr bool kDirectStores = false;
+  // layout need no LDS round trips but twice the store instructions;
+  // measured in one process against the staged form, they were 1-12 %
+  // slower on every tile shape.
   // stores per wave per tile on the fast paths (fp32: 16 bytes per (i, j, q))
-  constexpr int kStagedStores = (OUT == FR_DTYPE_FP32 || kDirectStores) ? 4 * FN * FM : 2 * FN * FM;
+  constexpr int kStagedStores = OUT == FR_DTYPE_FP32 ? 4 * FN * FM : 2 * FN * FM;
   // Returns whether a fast path ran (and so issued exactly kStagedStores
   // stores per wave).
   auto epilogue = [&](int64_t local) -> bool __attribute__((always_inline)) {
@@ -473,21 +472,26 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     // as 128-byte row segments: 16 KB a store instruction per 8 rows.  All
     // scales are read up front, in one LDS round trip.
     const uint32_t stg_base = lds_addr(stg);
-    u32x4 sb4[FN * 4];
+    // Passes t = (p, j), p outer: the column scales of one column pair
+    // (32 registers) stay loaded through its FM passes.
+    u32x4 sb4[8];
     float sam_r[FM];
+    auto load_sb = [&](int p) __attribute__((always_inline)) {
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (sb_vec) {
+            sb4[4 * ii + q] = lds_read_b128_nw(sbl + 128 * (2 * p + ii) + 32 * q);
+          } else {
+            const uint32_t b0 = __float_as_uint(sb0);
+            sb4[4 * ii + q] = u32x4{b0, b0, b0, b0};
+          }
+        }
+    };
 #pragma unroll
     for (int j = 0; j < FM; ++j) sam_r[j] = sa_vec ? lds_read_f32_nw(sal + 128 * j) : sa0;
-#pragma unroll
-    for (int i = 0; i < FN; ++i)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (sb_vec) {
-          sb4[4 * i + q] = lds_read_b128_nw(sbl + 128 * i + 32 * q);
-        } else {
-          const uint32_t b0 = __float_as_uint(sb0);
-          sb4[4 * i + q] = u32x4{b0, b0, b0, b0};
-        }
-      }
+    load_sb(0);
     lds_wait_all(sb4, sam_r);
     // Stores go through a buffer resource based at this wave's sub-tile: the
     // lane's offset is formed once, each store's row/column step is a scalar
@@ -499,62 +503,72 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
         make_rsrc(reinterpret_cast<const void*>((static_cast<uint64_t>(ohi) << 32) | olo), 0xFFFFFFFFu);
     const uint32_t ldo32 = static_cast<uint32_t>(g.ldo);
     const uint32_t vo = ((lx >> 3) * ldo32 + (lx & 7) * 8) * 2;
-    if constexpr (kDirectStores) {
-      // stores straight from the accumulator layout: lane l writes the 4
-      // outputs (8 bytes) of row l%32, columns 8q + 4(l/32) .. +3 of each block
-  #pragma unroll
-      for (int j = 0; j < FM; ++j) {
-        const float sam = sam_r[j];
-        uint16_t* orow = static_cast<uint16_t*>(g.out) + (m0 + j * 32 + row) * g.ldo + n0 + h4;
-  #pragma unroll
-        for (int i = 0; i < FN; ++i)
-  #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            float v[4];
-  #pragma unroll
-            for (int t = 0; t < 4; ++t) v[t] = (acc[i][j][4 * q + t] * sam) * __uint_as_float(sb4[4 * i + q][t]);
-            uint2 w;
-            w.x = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v[0], v[1]) : pack_fp16x2(v[0], v[1]);
-            w.y = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v[2], v[3]) : pack_fp16x2(v[2], v[3]);
-            *reinterpret_cast<uint2*>(orow + i * 32 + 8 * q) = w;
-          }
-      }
-    } else {
-  #pragma unroll
-      for (int j = 0; j < FM; ++j) {
-        const float sam = sam_r[j];
-  #pragma unroll
-        for (int p = 0; p < FN / 2; ++p) {
-  #pragma unroll
-          for (int ii = 0; ii < 2; ++ii) {
-            const int i = 2 * p + ii;
-  #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              float v[4];
-  #pragma unroll
-              for (int t = 0; t < 4; ++t) v[t] = (acc[i][j][4 * q + t] * sam) * __uint_as_float(sb4[4 * i + q][t]);
-              const uint32_t lo = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v[0], v[1]) : pack_fp16x2(v[0], v[1]);
-              const uint32_t hi = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v[2], v[3]) : pack_fp16x2(v[2], v[3]);
-              const int byte = 2 * (ii * 32 + 8 * q + h4);  // inside the 128-byte staging row
-              lds_write_b64(stg_base + row * 128 + ((((byte >> 4) ^ (row & 7))) << 4) + (byte & 15), lo, hi);
-            }
-          }
-          // read back: 8 lanes per 128-byte row, 8 rows per read
-          const int cg = lx & 7;
-          uint32_t ra[4];
-          int rr_row[4];
-  #pragma unroll
-          for (int rr = 0; rr < 4; ++rr) {
-            rr_row[rr] = rr * 8 + (lx >> 3);
-            ra[rr] = stg_base + rr_row[rr] * 128 + ((cg ^ (rr_row[rr] & 7)) << 4);
-          }
-          u32x4 w[4];
-          lds_read4_b128(ra[0], ra[1], ra[2], ra[3], w[0], w[1], w[2], w[3]);
-  #pragma unroll
-          for (int rr = 0; rr < 4; ++rr)
-            __builtin_amdgcn_raw_buffer_store_b128(w[rr], ro, vo,
-                                                   static_cast<int>(((j * 32 + rr * 8) * ldo32 + p * 64) * 2), 0);
+    // Passes t = (j, p) are software-pipelined: pass t+1's outputs are
+    // scaled and converted while pass t's staging reads are in flight.
+    constexpr int NP = FM * FN / 2;
+    const int cg = lx & 7;
+    uint32_t ra[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int r = rr * 8 + (lx >> 3);
+      ra[rr] = stg_base + r * 128 + ((cg ^ (r & 7)) << 4);
+    }
+    u32x2 pk[8];  // (ii, q): four converted outputs of the next pass
+    auto compute = [&](int t) __attribute__((always_inline)) {
+      const int j = t % FM, p = t / FM;
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int i = 2 * p + ii;
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = (acc[i][j][4 * q + e] * sam_r[j]) * __uint_as_float(sb4[4 * ii + q][e]);
+          pk[4 * ii + q][0] = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v[0], v[1]) : pack_fp16x2(v[0], v[1]);
+          pk[4 * ii + q][1] = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v[2], v[3]) : pack_fp16x2(v[2], v[3]);
         }
+    };
+    auto stage = [&]() __attribute__((always_inline)) {
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int byte = 2 * (ii * 32 + 8 * q + h4);  // inside the 128-byte staging row
+          lds_write_b64(stg_base + row * 128 + ((((byte >> 4) ^ (row & 7))) << 4) + (byte & 15),
+                        pk[4 * ii + q][0], pk[4 * ii + q][1]);
+        }
+    };
+    u32x4 w[4];
+    auto read_back = [&]() __attribute__((always_inline)) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) w[rr] = lds_read_b128_nw(ra[rr]);
+    };
+    compute(0);
+    stage();
+    read_back();
+#pragma unroll
+    for (int t = 0; t < NP; ++t) {
+      if (t + 1 < NP && (t + 1) % FM == 0) {
+        // next column pair: its scales replace this pair's (already applied)
+        load_sb((t + 1) / FM);
+        lds_wait_all(sb4, sam_r);
+      }
+      if (t + 1 < NP) compute(t + 1);
+      // one wait for the reads, taking the next pass's values as operands so
+      // their arithmetic stays ahead of it
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(pk[0]), "+v"(pk[1]), "+v"(pk[2]),
+                     "+v"(pk[3]), "+v"(pk[4]), "+v"(pk[5]), "+v"(pk[6]), "+v"(pk[7])
+                   :
+                   : "memory");
+      const int j = t % FM, p = t / FM;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+        __builtin_amdgcn_raw_buffer_store_b128(w[rr], ro, vo, static_cast<int>(((j * 32 + rr * 8) * ldo32 + p * 64) * 2),
+                                               0);
+      if (t + 1 < NP) {
+        stage();
+        read_back();
       }
     }
     return true;
