@@ -443,25 +443,86 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     const int h4 = 4 * (lx >> 5);
     const uint32_t sbl = lds_addr(scl + (local & 1) * 2048) + 4 * (wn * WN + h4);
     const uint32_t sal = lds_addr(scl + (local & 1) * 2048 + 1024) + 4 * (wm * WM + row);
-    if (OUT == FR_DTYPE_FP32) {
-      // 16 bytes per lane already: (i, j, q) -> row l%32, 4 columns
+    if constexpr (OUT == FR_DTYPE_FP32) {
+      // per pass (i, j): the block's 32 x 32 fp32 outputs go through the same
+      // 32 x 128-byte staging tile (lane l writes its four 16-byte column
+      // groups 8q + 4(l/32) of row l%32 to chunk (2q + l/32) ^ (row % 8)) and
+      // leave as 128-byte row segments; passes are pipelined as for bf16
+      const uint32_t stg_base = lds_addr(stg);
+      const uint64_t obase = reinterpret_cast<uint64_t>(static_cast<float*>(g.out) + m0 * g.ldo + n0);
+      const uint32_t olo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(obase));
+      const uint32_t ohi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(obase >> 32));
+      const __amdgpu_buffer_rsrc_t ro =
+          make_rsrc(reinterpret_cast<const void*>((static_cast<uint64_t>(ohi) << 32) | olo), 0xFFFFFFFFu);
+      const uint32_t ldo32 = static_cast<uint32_t>(g.ldo);
+      const uint32_t vo = ((lx >> 3) * ldo32 + (lx & 7) * 4) * 4;
+      float sam_r[FM];
+      u32x4 sb4[4];
+      auto load_sb = [&](int i) __attribute__((always_inline)) {
 #pragma unroll
-      for (int j = 0; j < FM; ++j) {
-        const float sam = sa_vec ? lds_read_f32(sal + 128 * j) : sa0;
-        float* orow = static_cast<float*>(g.out) + (m0 + j * 32 + row) * g.ldo + n0 + h4;
-#pragma unroll
-        for (int i = 0; i < FN; ++i) {
-          u32x4 sb4[4];
-          if (sb_vec) lds_read4_b128(sbl + 128 * i, sbl + 128 * i + 32, sbl + 128 * i + 64, sbl + 128 * i + 96,
-                                     sb4[0], sb4[1], sb4[2], sb4[3]);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            float v[4];
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-              v[t] = (acc[i][j][4 * q + t] * sam) * (sb_vec ? __uint_as_float(sb4[q][t]) : sb0);
-            *reinterpret_cast<float4*>(orow + i * 32 + 8 * q) = make_float4(v[0], v[1], v[2], v[3]);
+        for (int q = 0; q < 4; ++q) {
+          if (sb_vec) {
+            sb4[q] = lds_read_b128_nw(sbl + 128 * i + 32 * q);
+          } else {
+            const uint32_t b0 = __float_as_uint(sb0);
+            sb4[q] = u32x4{b0, b0, b0, b0};
           }
+        }
+      };
+#pragma unroll
+      for (int j = 0; j < FM; ++j) sam_r[j] = sa_vec ? lds_read_f32_nw(sal + 128 * j) : sa0;
+      load_sb(0);
+      lds_wait_all(sb4, sam_r);
+      constexpr int NP = FN * FM;
+      const int cg = lx & 7;
+      uint32_t ra[4];
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int r = rr * 8 + (lx >> 3);
+        ra[rr] = stg_base + r * 128 + ((cg ^ (r & 7)) << 4);
+      }
+      u32x4 pk[4];
+      auto compute = [&](int t) __attribute__((always_inline)) {
+        const int i = t / FM, j = t % FM;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            pk[q][e] = __float_as_uint((acc[i][j][4 * q + e] * sam_r[j]) * __uint_as_float(sb4[q][e]));
+      };
+      auto stage = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          lds_write_b128(stg_base + row * 128 + (((2 * q + (lx >> 5)) ^ (row & 7)) << 4), pk[q]);
+      };
+      u32x4 w[4];
+      auto read_back = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) w[rr] = lds_read_b128_nw(ra[rr]);
+      };
+      compute(0);
+      stage();
+      read_back();
+#pragma unroll
+      for (int t = 0; t < NP; ++t) {
+        if (t + 1 < NP && (t + 1) % FM == 0) {
+          load_sb((t + 1) / FM);
+          lds_wait_all(sb4, sam_r);
+        }
+        if (t + 1 < NP) compute(t + 1);
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(pk[0]), "+v"(pk[1]), "+v"(pk[2]),
+                       "+v"(pk[3])
+                     :
+                     : "memory");
+        const int i = t / FM, j = t % FM;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          __builtin_amdgcn_raw_buffer_store_b128(w[rr], ro, vo,
+                                                 static_cast<int>(((j * 32 + rr * 8) * ldo32 + i * 32) * 4), 0);
+        if (t + 1 < NP) {
+          stage();
+          read_back();
         }
       }
       return true;
