@@ -10,14 +10,15 @@
 // token per row in decode; in causal prefill, token j of a row with prefix P
 // sees P + j + 1.
 //
-// Two kernels share the work of one call, each taking whole groups of
-// 32 / NREP consecutive query tokens (32 query rows):
+// The work of one call goes in whole groups of 32 / NREP consecutive query
+// tokens (32 query rows):
 //  * paged_attn_grouped_d128 (bf16 MFMA) takes the groups whose tokens all
 //    see the same first 32 slots — beams of one request decoding over their
 //    shared prompt, the common case — and multiplies their shared slot
 //    prefix once for all 32 queries;
-//  * paged_attn_tokens_d128 takes every other group and attends token by
-//    token on the VALU (attend_token).
+//  * every other group is attended token by token on the VALU (attend_token):
+//    inside the same kernel for NREP < 8, by paged_attn_tokens_d128 (a
+//    second launch, more registers per wave) for NREP >= 8.
 // Arithmetic in fp32 (e4m3 and bf16 convert exactly; the MFMA path rounds the
 // probabilities to bf16, as the reference's bf16 SDPA does), output bf16.
 #include <type_traits>
@@ -328,6 +329,9 @@ __device__ __forceinline__ bf16x8_t e4m3x8_to_bf16(uint32_t w0, uint32_t w1) {
 constexpr int kVRow = 288;  // LDS bytes per staged V row: 256 + 32 (bank spread)
 
 template <int NREP>
+constexpr bool kSeparateTokenKernel = NREP >= 8;
+
+template <int NREP>
 __global__ __launch_bounds__(256, 2) void paged_attn_grouped_d128(AttnArgs a) {
   constexpr int TOK = 32 / NREP;  // tokens per group
   __shared__ __attribute__((aligned(16))) uint8_t lds[4 * 32 * kVRow];
@@ -338,8 +342,17 @@ __global__ __launch_bounds__(256, 2) void paged_attn_grouped_d128(AttnArgs a) {
   const int kh = static_cast<int>(item - group * a.Hk);
   const int64_t t0 = group * TOK;
   if (t0 >= a.T) return;
-  // groups without a shared 32-slot block go to paged_attn_tokens_d128
-  if (a.gp ? a.gp[group] == 0 : !group_shares_block<TOK>(a, t0, lane)) return;
+  // A group without a shared 32-slot block is attended token by token on
+  // the VALU: here, by this wave for its kv head, when the per-token
+  // registers fit two waves per SIMD (NREP < 8); otherwise by
+  // paged_attn_tokens_d128, a launch of its own.
+  if (a.gp ? a.gp[group] == 0 : !group_shares_block<TOK>(a, t0, lane)) {
+    if constexpr (!kSeparateTokenKernel<NREP>) {
+      const int ntok = static_cast<int>(min<int64_t>(TOK, a.T - t0));
+      for (int tt = 0; tt < ntok; ++tt) attend_token<NREP, 16 / NREP>(a, t0 + tt, kh, lane);
+    }
+    return;
+  }
   uint8_t* vs = lds + wave * (32 * kVRow);
   const int n = lane & 31;  // query column (and key row when loading)
   const int h = lane >> 5;  // half: dims 64h .. 64h + 63
@@ -390,14 +403,15 @@ __global__ __launch_bounds__(256, 2) void paged_attn_grouped_d128(AttnArgs a) {
   // Gathers are unconditional (an invalid row reads slot 0's bytes); scores
   // of invalid rows are masked below and their V rows zeroed, so nothing
   // from them (not even a NaN pattern) reaches the sums.
-  auto load = [&](int32_t bi, Loaded& L) __attribute__((always_inline)) {
-    int32_t slot = -1;
-    if (bi < nshared) {
-      slot = i0[32 * bi + n];
-    } else {
-      const int32_t pos = P32 + (bi - nshared) * NREP + n % NREP;
-      slot = (bi < nblocks && pos < klen) ? ik[pos] : -1;
-    }
+  // Slot of this lane's key row in block bi (-1: none).  Fetched one block
+  // ahead, so its load latency overlaps the previous block's work (holding
+  // the next block's row gathers in registers as well measured no faster).
+  auto slot_of = [&](int32_t bi) __attribute__((always_inline)) -> int32_t {
+    if (bi < nshared) return i0[32 * bi + n];
+    const int32_t pos = P32 + (bi - nshared) * NREP + n % NREP;
+    return (bi < nblocks && pos < klen) ? ik[pos] : -1;
+  };
+  auto load = [&](int32_t slot, Loaded& L) __attribute__((always_inline)) {
     L.ok = slot >= 0 && slot < a.num_slots;
     const int64_t sl = L.ok ? slot : 0;
     const uint8_t* kp = a.kc + sl * a.skp + kh * a.skh + 64 * h;
@@ -509,12 +523,15 @@ __global__ __launch_bounds__(256, 2) void paged_attn_grouped_d128(AttnArgs a) {
   // the other wave hides the gather latency (config-4 decode 62 -> 44 us).
   Loaded LA;
   int32_t bi = 0;
+  int32_t slot = nblocks > 0 ? slot_of(0) : -1;
   for (; bi < nshared; ++bi) {
-    load(bi, LA);
+    load(slot, LA);
+    if (bi + 1 < nblocks) slot = slot_of(bi + 1);
     compute(bi, LA, std::false_type{});
   }
   for (; bi < nblocks; ++bi) {
-    load(bi, LA);
+    load(slot, LA);
+    if (bi + 1 < nblocks) slot = slot_of(bi + 1);
     compute(bi, LA, std::true_type{});
   }
 
@@ -555,15 +572,17 @@ __global__ __launch_bounds__(64 * token_waves<NREP>()) void paged_attn_tokens_d1
     attend_token<NREP, NP>(a, t0 + p / a.Hk, static_cast<int>(p % a.Hk), lane);
 }
 
-// Two launches on the stream: every group is taken by exactly one of them.
+// One launch, or two for NREP >= 8 (the token path in a kernel of its own):
+// every group is taken by exactly one wave set.
 template <int NREP>
 static hipError_t launch_grouped(const AttnArgs& a, hipStream_t st) {
   const int64_t groups = (a.T + 32 / NREP - 1) / (32 / NREP);
   const int64_t items = groups * a.Hk;
   hipLaunchKernelGGL((paged_attn_grouped_d128<NREP>), dim3(static_cast<unsigned>((items + 3) / 4)),
                      dim3(256), 0, st, a);
-  hipLaunchKernelGGL((paged_attn_tokens_d128<NREP>), dim3(static_cast<unsigned>(groups)),
-                     dim3(64 * token_waves<NREP>()), 0, st, a);
+  if (kSeparateTokenKernel<NREP>)
+    hipLaunchKernelGGL((paged_attn_tokens_d128<NREP>), dim3(static_cast<unsigned>(groups)),
+                       dim3(64 * token_waves<NREP>()), 0, st, a);
   return hipGetLastError();
 }
 
