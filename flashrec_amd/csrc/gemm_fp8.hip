@@ -28,6 +28,8 @@
 //  * Workgroup -> tile mapping is XCD aware: dispatch places workgroup i on
 //    XCD i % 8; tiles are renumbered so each XCD walks a contiguous, m-grouped
 //    range and its 32 CUs share weight/activation panels in their L2.
+#include <type_traits>
+
 #include "fr_common.h"
 
 namespace fr {
@@ -64,6 +66,15 @@ __device__ __forceinline__ int swz_g(int r) {
   return ((r >> 2) & 1) | ((((r >> 1) ^ (r >> 3)) & 1) << 1);
 }
 __device__ __forceinline__ int swz(int r, int c) { return r * 64 + ((c ^ swz_g(r)) << 4); }
+// 128-byte rows (8 chunks): chunk c of row r in slot c ^ ((r / 2) % 8).  A
+// 256-byte bank line holds two rows, so any 16 consecutive rows read at one
+// logical chunk fall on 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int swz_g8(int r) { return (r >> 1) & 7; }
+template <int RB>
+__device__ __forceinline__ int swz_row(int r, int c) {
+  if constexpr (RB == 64) return swz(r, c);
+  else return r * 128 + ((c ^ swz_g8(r)) << 4);
+}
 
 // Workgroup barrier that orders LDS accesses only.  __syncthreads() would
 // also wait for every outstanding global->LDS load (vmcnt(0)) and so drain
@@ -223,9 +234,11 @@ __device__ __forceinline__ void tile_coords(int64_t pid, int64_t nt, int64_t til
 }
 
 // BN: weight rows (output columns) per tile, BM: activation rows per tile,
-// NST: LDS ring depth in 64-byte K steps, KTAIL: K % 128 != 0 (the last
-// K steps are partly or wholly zero-filled).
-template <int BN, int BM, int NST, int OUT, bool KTAIL>
+// RB: bytes of K per LDS row (64: one MFMA K step per ring slot, 128: two,
+// so each direct-to-LDS load covers whole 128-byte lines), NSL: ring depth
+// in slots, KTAIL: K % 128 != 0 (the last K steps are partly or wholly
+// zero-filled).
+template <int BN, int BM, int NSL, int RB, int OUT, bool KTAIL>
 __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   // The host pass only needs the kernel's signature (for its launch stub);
   // the body uses device-only buffer-resource builtins.
@@ -234,15 +247,20 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   constexpr int FM = BM / 64;  // 32-row blocks per wave along m
   constexpr int WN = BN / 2;   // wave sub-tile: WN output columns ...
   constexpr int WM = BM / 2;   // ... x WM output rows
-  constexpr int IB = BN / 64;  // 1 KB direct-to-LDS loads per wave per K step (weights)
-  constexpr int IA = BM / 64;  // ... (activations)
-  constexpr int STAGE = (BN + BM) * kBK;
-  constexpr int LOADS = IB + IA;  // vmcnt units one K step adds per wave
+  constexpr int SPS = RB / kBK;       // MFMA K steps per ring slot
+  constexpr int RPI = 1024 / RB;      // rows one 1 KB direct-to-LDS load covers
+  constexpr int CPR = RB / 16;        // 16-byte chunks per LDS row
+  constexpr int IB = BN * RB / 4096;  // 1 KB loads per wave per slot (weights)
+  constexpr int IA = BM * RB / 4096;  // ... (activations)
+  constexpr int STAGE = (BN + BM) * RB;
+  constexpr int LOADS = IB + IA;  // vmcnt units one slot adds per wave
   constexpr int EB = OutT<OUT>::kBytes;
-  // LDS: the K-step ring, per-wave epilogue staging, two 2 KB scale buffers
-  constexpr int STG = 32 * 128;  // epilogue staging per wave: 32 rows x 128 bytes
-  // LDS: the K-step ring, two 2 KB scale buffers, per-wave epilogue staging
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * STAGE + 2 * 2048 + 4 * STG];
+  // LDS: the slot ring, two 2 KB scale buffers, per-wave epilogue staging of
+  // 32 rows x 128 bytes, or x 64 bytes where the wider staging does not fit
+  constexpr bool kNarrow = NSL * STAGE + 2 * 2048 + 4 * 32 * 128 > 160 * 1024;
+  constexpr int SRB = kNarrow ? 64 : 128;  // staging row bytes
+  constexpr int STG = 32 * SRB;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NSL * STAGE + 2 * 2048 + 4 * STG];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -258,6 +276,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   // K steps per tile, rounded up to even (steps run in pairs); steps past
   // K read zeros through the buffer range check.
   const int KT = static_cast<int>((g.K + 2 * kBK - 1) / (2 * kBK)) * 2;
+  const int KS = KT / SPS;  // ring slots per tile
   const int64_t S = my_tiles * KT;  // K steps this workgroup runs
   if (S == 0) return;
 
@@ -266,23 +285,27 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   const __amdgpu_buffer_rsrc_t ra =
       make_rsrc(g.a, static_cast<uint32_t>((g.M - 1) * g.lda + g.K));
 
-  // ---- direct-to-LDS loads.  One wave instruction fills 1 KB = 16 rows of
-  // 64 B; lane L lands in row L/4, chunk slot L%4, so it fetches the global
-  // chunk (L%4) ^ g(L/4).  Per-lane row offsets are kept for the tile being
+  // ---- direct-to-LDS loads.  One wave instruction fills 1 KB = RPI rows of
+  // RB bytes; lane L lands in row L/CPR, chunk slot L%CPR, so it fetches the
+  // global chunk (L%CPR) ^ g(L/CPR).  Per-lane row offsets are kept for the tile being
   // computed (cur) and the next one (nxt): the ring runs NST steps ahead, so
   // the last NST steps of a tile load the first ones of the next.  Offsets of
   // a tile past the end are out of range (loads return zeros, touch nothing).
-  const int lrow = lane >> 2;
-  const int lchunk = (lane & 3) ^ swz_g(lrow);
+  // The swizzle depends on row bits 0-3.  A load covers 16 (RB = 64) or 8
+  // (RB = 128) rows starting at a multiple of 16 or 8: in the second case
+  // bit 3 of the row is the parity of the load's index l*4 + wave, i.e. of
+  // the wave.
+  const int lrow = lane / CPR;
+  const int lchunk = (lane % CPR) ^ (RB == 64 ? swz_g(lrow) : swz_g8(lrow + 8 * (wave & 1)));
   constexpr uint32_t kOOB = 0x80000000u;
   // Per-lane part of each load's offset (the same for every tile) and the
   // scalar tile bases of the current and the next tile; a tile past the end
   // gets base kOOB (the sum is then past the buffer: zeros, no access).
   uint32_t lob[IB], loa[IA];
 #pragma unroll
-  for (int i = 0; i < IB; ++i) lob[i] = static_cast<uint32_t>(((i * 4 + wave) * 16 + lrow) * g.ldb + lchunk * 16);
+  for (int i = 0; i < IB; ++i) lob[i] = static_cast<uint32_t>(((i * 4 + wave) * RPI + lrow) * g.ldb + lchunk * 16);
 #pragma unroll
-  for (int i = 0; i < IA; ++i) loa[i] = static_cast<uint32_t>(((i * 4 + wave) * 16 + lrow) * g.lda + lchunk * 16);
+  for (int i = 0; i < IA; ++i) loa[i] = static_cast<uint32_t>(((i * 4 + wave) * RPI + lrow) * g.lda + lchunk * 16);
   uint32_t bb_cur, ba_cur, bb_nxt, ba_nxt;
   auto tile_bases = [&](int64_t local, uint32_t& bb, uint32_t& ba) __attribute__((always_inline)) {
     if (local >= my_tiles) {
@@ -294,12 +317,12 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     bb = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(tn * BN * g.ldb));
     ba = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(tm * BM * g.lda));
   };
-  // Load `l` (0..LOADS-1: weight blocks, then activation blocks) of K step
-  // `lk` (0..KT-1) of the cur or nxt tile into `slot`.
+  // Load `l` (0..LOADS-1: weight blocks, then activation blocks) of ring
+  // slot `lk` (0..KS-1, RB bytes of K) of the cur or nxt tile into `slot`.
   auto issue_one = [&](int slot, int lk, bool next, int l) __attribute__((always_inline)) {
     uint8_t* sb = smem + slot * STAGE;
-    uint8_t* sa = sb + BN * kBK;
-    const uint32_t k0 = static_cast<uint32_t>(lk) * kBK;
+    uint8_t* sa = sb + BN * RB;
+    const uint32_t k0 = static_cast<uint32_t>(lk) * RB;
     const bool kin = !KTAIL || (k0 + lchunk * 16 < static_cast<uint64_t>(g.K));
     if (l < IB) {
       const uint32_t o = lob[l] + (next ? bb_nxt : bb_cur);
@@ -335,21 +358,23 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     if constexpr (kOneB) return fb1[i][h];
     else return f.b[i][h];
   };
-  auto read_one = [&](Frags& f, int slot, int r) __attribute__((always_inline)) {
+  // Fragments of MFMA K step `sub` (0..SPS-1) of a ring slot.
+  auto read_one = [&](Frags& f, int slot, int sub, int r) __attribute__((always_inline)) {
     const uint8_t* sb = smem + slot * STAGE;
-    const uint8_t* sa = sb + BN * kBK;
+    const uint8_t* sa = sb + BN * RB;
     const int h = r & 1;
+    const int c = 4 * sub + c0 + h;
     if (r < 2 * FN) {
       const int i = r >> 1;
-      breg(f, i, h) = *reinterpret_cast<const u32x4*>(sb + swz(wn * WN + i * 32 + fr, c0 + h));
+      breg(f, i, h) = *reinterpret_cast<const u32x4*>(sb + swz_row<RB>(wn * WN + i * 32 + fr, c));
     } else {
       const int j = (r >> 1) - FN;
-      f.a[j][h] = *reinterpret_cast<const u32x4*>(sa + swz(wm * WM + j * 32 + fr, c0 + h));
+      f.a[j][h] = *reinterpret_cast<const u32x4*>(sa + swz_row<RB>(wm * WM + j * 32 + fr, c));
     }
   };
-  auto read_frags = [&](Frags& f, int slot) __attribute__((always_inline)) {
+  auto read_frags = [&](Frags& f, int slot, int sub) __attribute__((always_inline)) {
 #pragma unroll
-    for (int r = 0; r < 2 * (FN + FM); ++r) read_one(f, slot, r);
+    for (int r = 0; r < 2 * (FN + FM); ++r) read_one(f, slot, sub, r);
   };
   v16f acc[FN][FM];
   // A tile's first K step starts its accumulators from the constant 0
@@ -371,8 +396,8 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   // so the epilogue issues no global load (a load here would queue behind
   // the next tile's ring loads: vmcnt retires in order) and holds no scale
   // registers through the K loop.
-  uint8_t* const scl = smem + NST * STAGE;
-  uint8_t* const stg = smem + NST * STAGE + 2 * 2048 + wave * STG;
+  uint8_t* const scl = smem + NSL * STAGE;
+  uint8_t* const stg = smem + NSL * STAGE + 2 * 2048 + wave * STG;
   // scales: sb[BN] (1 KB) then sa[BM] (1 KB) as fp32, one buffer per tile parity
   const bool sa_vec = g.sa_stride != 0, sb_vec = g.sb_stride != 0;
   // per-tensor scales, read once up front (never a load in the epilogue)
@@ -443,166 +468,114 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     const int h4 = 4 * (lx >> 5);
     const uint32_t sbl = lds_addr(scl + (local & 1) * 2048) + 4 * (wn * WN + h4);
     const uint32_t sal = lds_addr(scl + (local & 1) * 2048 + 1024) + 4 * (wm * WM + row);
-    if constexpr (OUT == FR_DTYPE_FP32) {
-      // per pass (i, j): the block's 32 x 32 fp32 outputs go through the same
-      // 32 x 128-byte staging tile (lane l writes its four 16-byte column
-      // groups 8q + 4(l/32) of row l%32 to chunk (2q + l/32) ^ (row % 8)) and
-      // leave as 128-byte row segments; passes are pipelined as for bf16
-      const uint32_t stg_base = lds_addr(stg);
-      const uint64_t obase = reinterpret_cast<uint64_t>(static_cast<float*>(g.out) + m0 * g.ldo + n0);
-      const uint32_t olo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(obase));
-      const uint32_t ohi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(obase >> 32));
-      const __amdgpu_buffer_rsrc_t ro =
-          make_rsrc(reinterpret_cast<const void*>((static_cast<uint64_t>(ohi) << 32) | olo), 0xFFFFFFFFu);
-      const uint32_t ldo32 = static_cast<uint32_t>(g.ldo);
-      const uint32_t vo = ((lx >> 3) * ldo32 + (lx & 7) * 4) * 4;
-      float sam_r[FM];
-      u32x4 sb4[4];
-      auto load_sb = [&](int i) __attribute__((always_inline)) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (sb_vec) {
-            sb4[q] = lds_read_b128_nw(sbl + 128 * i + 32 * q);
-          } else {
-            const uint32_t b0 = __float_as_uint(sb0);
-            sb4[q] = u32x4{b0, b0, b0, b0};
-          }
-        }
-      };
-#pragma unroll
-      for (int j = 0; j < FM; ++j) sam_r[j] = sa_vec ? lds_read_f32_nw(sal + 128 * j) : sa0;
-      load_sb(0);
-      lds_wait_all(sb4, sam_r);
-      constexpr int NP = FN * FM;
-      const int cg = lx & 7;
-      uint32_t ra[4];
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int r = rr * 8 + (lx >> 3);
-        ra[rr] = stg_base + r * 128 + ((cg ^ (r & 7)) << 4);
-      }
-      u32x4 pk[4];
-      auto compute = [&](int t) __attribute__((always_inline)) {
-        const int i = t / FM, j = t % FM;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            pk[q][e] = __float_as_uint((acc[i][j][4 * q + e] * sam_r[j]) * __uint_as_float(sb4[q][e]));
-      };
-      auto stage = [&]() __attribute__((always_inline)) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          lds_write_b128(stg_base + row * 128 + (((2 * q + (lx >> 5)) ^ (row & 7)) << 4), pk[q]);
-      };
-      u32x4 w[4];
-      auto read_back = [&]() __attribute__((always_inline)) {
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) w[rr] = lds_read_b128_nw(ra[rr]);
-      };
-      compute(0);
-      stage();
-      read_back();
-#pragma unroll
-      for (int t = 0; t < NP; ++t) {
-        if (t + 1 < NP && (t + 1) % FM == 0) {
-          load_sb((t + 1) / FM);
-          lds_wait_all(sb4, sam_r);
-        }
-        if (t + 1 < NP) compute(t + 1);
-        asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(pk[0]), "+v"(pk[1]), "+v"(pk[2]),
-                       "+v"(pk[3])
-                     :
-                     : "memory");
-        const int i = t / FM, j = t % FM;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          __builtin_amdgcn_raw_buffer_store_b128(w[rr], ro, vo,
-                                                 static_cast<int>(((j * 32 + rr * 8) * ldo32 + i * 32) * 4), 0);
-        if (t + 1 < NP) {
-          stage();
-          read_back();
-        }
-      }
-      return true;
-    }
-    // bf16 / fp16: per pass (j, two column blocks) the converted outputs go
-    // to a 32 x 128-byte staging tile (16-byte chunk c of row r at slot
-    // c ^ (r % 8)), are read back as 16 consecutive bytes per lane and stored
-    // as 128-byte row segments: 16 KB a store instruction per 8 rows.  All
-    // scales are read up front, in one LDS round trip.
+    // Passes of 32 rows x SRB bytes: pass t = (column group cg, block row j),
+    // cg outer, covering CPP output columns (NQ groups u of 8: lane l holds
+    // columns 8u + 4(l/32) .. +3 of its row l%32).  The converted outputs go
+    // to the wave's staging tile (16-byte chunk c of row r at slot
+    // c ^ (r % CPRS)), are read back as 16 consecutive bytes per lane and
+    // stored as whole SRB-byte row segments.  Passes are software-pipelined:
+    // pass t+1 is scaled and converted while pass t's reads are in flight.
+    constexpr int CPP = SRB / EB;        // output columns per pass
+    constexpr int NQ = CPP / 8;          // 8-column groups per pass
+    constexpr int NCG = WN / CPP;        // column groups per wave
+    constexpr int NP = NCG * FM;         // passes
+    constexpr int CPRS = SRB / 16;       // 16-byte chunks per staging row (= lanes per row on read-back)
+    constexpr int RPR = 64 / CPRS;       // rows per read-back instruction
+    constexpr int NR = 32 / RPR;         // read-backs (and stores) per pass
+    static_assert(NP * NR == kStagedStores, "store count per tile");
+    using PkT = typename std::conditional<EB == 4, u32x4, u32x2>::type;
     const uint32_t stg_base = lds_addr(stg);
-    // Passes t = (p, j), p outer: the column scales of one column pair
-    // (32 registers) stay loaded through its FM passes.
-    u32x4 sb4[8];
-    float sam_r[FM];
-    auto load_sb = [&](int p) __attribute__((always_inline)) {
-#pragma unroll
-      for (int ii = 0; ii < 2; ++ii)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (sb_vec) {
-            sb4[4 * ii + q] = lds_read_b128_nw(sbl + 128 * (2 * p + ii) + 32 * q);
-          } else {
-            const uint32_t b0 = __float_as_uint(sb0);
-            sb4[4 * ii + q] = u32x4{b0, b0, b0, b0};
-          }
-        }
-    };
-#pragma unroll
-    for (int j = 0; j < FM; ++j) sam_r[j] = sa_vec ? lds_read_f32_nw(sal + 128 * j) : sa0;
-    load_sb(0);
-    lds_wait_all(sb4, sam_r);
-    // Stores go through a buffer resource based at this wave's sub-tile: the
+    // stores through a buffer resource based at this wave's sub-tile: the
     // lane's offset is formed once, each store's row/column step is a scalar
-    // offset (no 64-bit address arithmetic per store).
-    const uint64_t obase = reinterpret_cast<uint64_t>(static_cast<uint16_t*>(g.out) + m0 * g.ldo + n0);
+    // offset (no 64-bit address arithmetic per store)
+    const uint64_t obase = reinterpret_cast<uint64_t>(static_cast<uint8_t*>(g.out) + (m0 * g.ldo + n0) * EB);
     const uint32_t olo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(obase));
     const uint32_t ohi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(obase >> 32));
     const __amdgpu_buffer_rsrc_t ro =
         make_rsrc(reinterpret_cast<const void*>((static_cast<uint64_t>(ohi) << 32) | olo), 0xFFFFFFFFu);
     const uint32_t ldo32 = static_cast<uint32_t>(g.ldo);
-    const uint32_t vo = ((lx >> 3) * ldo32 + (lx & 7) * 8) * 2;
-    // Passes t = (j, p) are software-pipelined: pass t+1's outputs are
-    // scaled and converted while pass t's staging reads are in flight.
-    constexpr int NP = FM * FN / 2;
-    const int cg = lx & 7;
-    uint32_t ra[4];
+    const uint32_t vo = ((lx / CPRS) * ldo32 + (lx % CPRS) * (16 / EB)) * EB;
+    uint32_t ra[NR];
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int r = rr * 8 + (lx >> 3);
-      ra[rr] = stg_base + r * 128 + ((cg ^ (r & 7)) << 4);
+    for (int rr = 0; rr < NR; ++rr) {
+      const int r = rr * RPR + lx / CPRS;
+      ra[rr] = stg_base + r * SRB + (((lx % CPRS) ^ (r % CPRS)) << 4);
     }
-    u32x2 pk[8];  // (ii, q): four converted outputs of the next pass
-    auto compute = [&](int t) __attribute__((always_inline)) {
-      const int j = t % FM, p = t / FM;
+    // scales: sa of the wave's rows up front, sb per column group
+    u32x4 sb4[NQ];
+    float sam_r[FM];
+    auto load_sb = [&](int cg) __attribute__((always_inline)) {
 #pragma unroll
-      for (int ii = 0; ii < 2; ++ii)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int i = 2 * p + ii;
-          float v[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = (acc[i][j][4 * q + e] * sam_r[j]) * __uint_as_float(sb4[4 * ii + q][e]);
-          pk[4 * ii + q][0] = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v[0], v[1]) : pack_fp16x2(v[0], v[1]);
-          pk[4 * ii + q][1] = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v[2], v[3]) : pack_fp16x2(v[2], v[3]);
+      for (int u = 0; u < NQ; ++u) {
+        if (sb_vec) {
+          sb4[u] = lds_read_b128_nw(sbl + 4 * (cg * CPP + 8 * u));
+        } else {
+          const uint32_t b0 = __float_as_uint(sb0);
+          sb4[u] = u32x4{b0, b0, b0, b0};
         }
+      }
+    };
+#pragma unroll
+    for (int j = 0; j < FM; ++j) sam_r[j] = sa_vec ? lds_read_f32_nw(sal + 128 * j) : sa0;
+    load_sb(0);
+    lds_wait_all(sb4, sam_r);
+    PkT pk[NQ];
+    auto compute = [&](int t) __attribute__((always_inline)) {
+      const int cg = t / FM, j = t % FM;
+#pragma unroll
+      for (int u = 0; u < NQ; ++u) {
+        const int col = cg * CPP + 8 * u;
+        const int i = col / 32, q = (col % 32) / 8;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (acc[i][j][4 * q + e] * sam_r[j]) * __uint_as_float(sb4[u][e]);
+        if constexpr (EB == 4) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) pk[u][e] = __float_as_uint(v[e]);
+        } else {
+          pk[u][0] = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v[0], v[1]) : pack_fp16x2(v[0], v[1]);
+          pk[u][1] = OUT == FR_DTYPE_BF16 ? pack_bf16x2(v[2], v[3]) : pack_fp16x2(v[2], v[3]);
+        }
+      }
     };
     auto stage = [&]() __attribute__((always_inline)) {
 #pragma unroll
-      for (int ii = 0; ii < 2; ++ii)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int byte = 2 * (ii * 32 + 8 * q + h4);  // inside the 128-byte staging row
-          lds_write_b64(stg_base + row * 128 + ((((byte >> 4) ^ (row & 7))) << 4) + (byte & 15),
-                        pk[4 * ii + q][0], pk[4 * ii + q][1]);
-        }
+      for (int u = 0; u < NQ; ++u) {
+        const int byte = (8 * u + h4) * EB;  // inside the staging row
+        const uint32_t ad = stg_base + row * SRB + ((((byte >> 4) ^ (row % CPRS))) << 4) + (byte & 15);
+        if constexpr (EB == 4) lds_write_b128(ad, pk[u]);
+        else lds_write_b64(ad, pk[u][0], pk[u][1]);
+      }
     };
-    u32x4 w[4];
+    u32x4 w[NR];
     auto read_back = [&]() __attribute__((always_inline)) {
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) w[rr] = lds_read_b128_nw(ra[rr]);
+      for (int rr = 0; rr < NR; ++rr) w[rr] = lds_read_b128_nw(ra[rr]);
+    };
+    // one wait for the reads, taking the next pass's values as operands so
+    // their arithmetic stays ahead of it
+    auto wait_reads = [&]() __attribute__((always_inline)) {
+      if constexpr (NR == 4 && NQ == 8)
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(pk[0]), "+v"(pk[1]), "+v"(pk[2]),
+                       "+v"(pk[3]), "+v"(pk[4]), "+v"(pk[5]), "+v"(pk[6]), "+v"(pk[7])
+                     :
+                     : "memory");
+      else if constexpr (NR == 4 && NQ == 4)
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(pk[0]), "+v"(pk[1]), "+v"(pk[2]),
+                       "+v"(pk[3])
+                     :
+                     : "memory");
+      else if constexpr (NR == 2 && NQ == 4)
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(w[0]), "+v"(w[1]), "+v"(pk[0]), "+v"(pk[1]), "+v"(pk[2]), "+v"(pk[3])
+                     :
+                     : "memory");
+      else if constexpr (NR == 2 && NQ == 2)
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(w[0]), "+v"(w[1]), "+v"(pk[0]), "+v"(pk[1]) : : "memory");
+      else
+        static_assert(NR == 0, "pass shape");
     };
     compute(0);
     stage();
@@ -610,23 +583,17 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
 #pragma unroll
     for (int t = 0; t < NP; ++t) {
       if (t + 1 < NP && (t + 1) % FM == 0) {
-        // next column pair: its scales replace this pair's (already applied)
+        // next column group: its scales replace this group's (already applied)
         load_sb((t + 1) / FM);
         lds_wait_all(sb4, sam_r);
       }
       if (t + 1 < NP) compute(t + 1);
-      // one wait for the reads, taking the next pass's values as operands so
-      // their arithmetic stays ahead of it
-      asm volatile("s_waitcnt lgkmcnt(0)"
-                   : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(pk[0]), "+v"(pk[1]), "+v"(pk[2]),
-                     "+v"(pk[3]), "+v"(pk[4]), "+v"(pk[5]), "+v"(pk[6]), "+v"(pk[7])
-                   :
-                   : "memory");
-      const int j = t % FM, p = t / FM;
+      wait_reads();
+      const int cg = t / FM, j = t % FM;
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-        __builtin_amdgcn_raw_buffer_store_b128(w[rr], ro, vo, static_cast<int>(((j * 32 + rr * 8) * ldo32 + p * 64) * 2),
-                                               0);
+      for (int rr = 0; rr < NR; ++rr)
+        __builtin_amdgcn_raw_buffer_store_b128(w[rr], ro, vo,
+                                               static_cast<int>(((j * 32 + rr * RPR) * ldo32 + cg * CPP) * EB), 0);
       if (t + 1 < NP) {
         stage();
         read_back();
@@ -635,65 +602,68 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     return true;
   };
 
-  // ---- prologue: the first NST steps in flight; all but the last landed.
-  // With more than one tile per workgroup KT >= NST (see launch_mfma), so
-  // the prologue stays inside tile 0; with one tile, steps past its end are
+  // ---- prologue: the first NSL slots in flight; all but the last landed.
+  // With more than one tile per workgroup KS >= NSL (see launch_mfma), so
+  // the prologue stays inside tile 0; with one tile, slots past its end are
   // all-zero dummies.
   tile_bases(0, bb_cur, ba_cur);
   tile_bases(1, bb_nxt, ba_nxt);
   load_scales(0);
 #pragma unroll
-  for (int st = 0; st < NST; ++st) issue(st, st < KT ? st : st - KT, st >= KT);
+  for (int st = 0; st < NSL; ++st) issue(st, st < KS ? st : st - KS, st >= KS);
   waitcnt_vm<LOADS>();
   lds_barrier();
   Frags f0, f1;
-  read_frags(f0, 0);
+  read_frags(f0, 0, 0);
 
-  // ---- main loop.  Step s (tile s / KT, K step kt = s % KT) holds its
-  // fragments in `cur`.  It first waits for step s+1's slot (own loads, then
-  // everyone's through the barrier, which also retires every wave's reads of
-  // slot s % NST, read into registers during step s-1), refills that slot
-  // with step s+NST, and then runs all of its MFMAs with step s+1's fragment
-  // reads spread over the first three quarters of them and the refill loads
-  // over the last three quarters, so the LDS reads of the CU's four waves
-  // overlap the matrix work instead of stalling the next step.  Every step has the same shape:
-  // past the end the ring loads zeros and the last fragment read is
-  // discarded.
+  // ---- main loop.  Step s (tile s / KT, K step kt = s % KT; ring slot
+  // q = s / SPS, step s % SPS inside it) holds its fragments in `cur` and
+  // reads step s+1's into `nxt`.  The last step of a slot first waits for
+  // the next slot (own loads, then everyone's through the barrier, which also
+  // retires every wave's reads of slot q, whose steps are all in registers
+  // by then), refills slot q with slot q+NSL, and spreads those loads over
+  // its MFMAs.  Each MFMA is followed by its share of the next step's
+  // fragment reads (over the first three quarters) and of the refill loads
+  // (from the first quarter on), so the LDS reads of the CU's four waves
+  // overlap the matrix work instead of stalling the next step.  Past the end
+  // the ring loads zeros and the last fragment read is discarded.
   //
   // vmcnt retires loads and stores in issue order, so a plain load wait issued
   // while the epilogue's stores are in flight would also wait for them.
-  // Before a tile's epilogue every ring load but the newest step's is drained
-  // (waitcnt_vm<LOADS>), so the first two steps of the next tile skip the
-  // wait, and the steps up to NST-2 use a count that also leaves the
-  // epilogue's stores in flight (wait kind 2 below).  Requires NST >= 4.
-  static_assert(NST >= 4, "two wait-free steps need a 4-deep ring");
+  // Before a tile's epilogue every ring load but the newest slot's is drained
+  // (waitcnt_vm<LOADS>): slots 0..NSL-2 of the next tile have landed and
+  // need no wait; slot NSL-1 is waited for with a count that also leaves the
+  // epilogue's stores in flight (wait kind 2 below) when their number is
+  // known.
+  static_assert(NSL >= 2, "ring of at least two slots");
   constexpr int NMF = FN * FM;                   // MFMAs per step
   constexpr int NRD = 2 * (FN + FM);             // 16-byte LDS reads per step
   // Measured on the 4096-row gate_up and down shapes: these placements beat
   // reads over the first half and loads from the first MFMA or from the half.
   constexpr int RDU = NMF * 3 / 4;  // MFMAs the fragment reads spread over
   constexpr int LD0 = NMF / 4;      // first MFMA followed by a ring load
-  // Wait kinds: 0 none, 1 the step's loads (the NST-2 newer steps' loads may
+  // Wait kinds: 0 none, 1 the slot's loads (the NSL-2 newer slots' loads may
   // be in flight), 2 the same with the previous tile's staged stores also
-  // allowed in flight (they were issued after the loads waited for).
-
-  // The count is capped at vmcnt's 63: a smaller count only waits for the
+  // allowed in flight (they were issued after the loads waited for).  The
+  // count is capped at vmcnt's 63: a smaller count only waits for the
   // oldest few stores as well (conservative).
-  constexpr int kAdjN = (NST - 2) * LOADS + kStagedStores < 63 ? (NST - 2) * LOADS + kStagedStores : 63;
-  constexpr bool kCanAdjust = true;
-  auto step = [&](Frags& cur, Frags& nxt, int64_t s, int kt, int wait, bool first)
+  constexpr int kAdjN = (NSL - 2) * LOADS + kStagedStores < 63 ? (NSL - 2) * LOADS + kStagedStores : 63;
+  auto step = [&](Frags& cur, Frags& nxt, int64_t s, int kt, int wait, bool first, bool last)
       __attribute__((always_inline)) {
     __builtin_amdgcn_sched_barrier(0);
-    if (kCanAdjust && wait == 2)
-      waitcnt_vm<kAdjN>();
-    else if (wait != 0)
-      waitcnt_vm<(NST - 2) * LOADS>();
-    lds_barrier();
-    const int lk0 = kt + NST;
-    const int lk = lk0 < KT ? lk0 : lk0 - KT;
-    const bool nx = lk0 >= KT;
-    const int slot = static_cast<int>(s % NST);
-    const int nslot = static_cast<int>((s + 1) % NST);
+    if (last) {
+      if (wait == 2)
+        waitcnt_vm<kAdjN>();
+      else if (wait != 0)
+        waitcnt_vm<(NSL - 2) * LOADS>();
+      lds_barrier();
+    }
+    const int lq0 = kt / SPS + NSL;
+    const int lq = lq0 < KS ? lq0 : lq0 - KS;
+    const bool nx = lq0 >= KS;
+    const int slot = static_cast<int>((s / SPS) % NSL);
+    const int nslot = static_cast<int>(((s + 1) / SPS) % NSL);
+    const int nsub = static_cast<int>((s + 1) % SPS);
     // Unit u: its share of step s+1's fragment reads, MFMA u of step s
     // (weight block u / FM), with a single weight set the next weight block's
     // reads once its last MFMA is issued, its share of the refill loads.  The
@@ -705,37 +675,44 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
       if constexpr (kOneB) {
 #pragma unroll
         for (int r = 0; r < 2 * FM; ++r)
-          if (r * RDU / (2 * FM) == u) read_one(nxt, nslot, 2 * FN + r);
+          if (r * RDU / (2 * FM) == u) read_one(nxt, nslot, nsub, 2 * FN + r);
       } else {
 #pragma unroll
         for (int r = 0; r < NRD; ++r)
-          if (r * RDU / NRD == u) read_one(nxt, nslot, r);
+          if (r * RDU / NRD == u) read_one(nxt, nslot, nsub, r);
       }
       mfma_one(cur, u / FM, u % FM, first);
       if (kOneB && u % FM == FM - 1) {
-        read_one(nxt, nslot, 2 * (u / FM));
-        read_one(nxt, nslot, 2 * (u / FM) + 1);
+        read_one(nxt, nslot, nsub, 2 * (u / FM));
+        read_one(nxt, nslot, nsub, 2 * (u / FM) + 1);
       }
+      if (last) {
 #pragma unroll
-      for (int l = 0; l < LOADS; ++l)
-        if (LD0 + l * (NMF - LD0) / LOADS == u) issue_one(slot, lk, nx, l);
+        for (int l = 0; l < LOADS; ++l)
+          if (LD0 + l * (NMF - LD0) / LOADS == u) issue_one(slot, lq, nx, l);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  // A step's slot was loaded NST-1 steps earlier; for steps 2 .. NST-2 of a
-  // tile that lies before the previous tile's epilogue, whose stores then sit
-  // between those loads and the newest ones in the vmcnt order.  After a
-  // staged epilogue (a known store count) those steps allow the stores in
-  // flight; after any other (or none) they wait for them.
+  // Wait kind of the slot-final step kt of a tile: the slot after it is
+  // slot kt / SPS + 1 of the tile.
+  auto wait_kind = [&](int kt, bool staged_prev) __attribute__((always_inline)) -> int {
+    const int nq = kt / SPS + 1;
+    if (nq <= NSL - 2) return 0;
+    if (nq == NSL - 1) return staged_prev ? 2 : 1;
+    return 1;
+  };
   int64_t s = 0;
   bool staged_prev = false;
   for (int64_t tile = 0; tile < my_tiles; ++tile) {
-    step(f0, f1, s, 0, 0, true);
-    step(f1, f0, s + 1, 1, 0, false);
+    // steps run in pairs (f0, f1); with two steps per slot the second of a
+    // pair ends the slot
+    step(f0, f1, s, 0, SPS == 1 ? wait_kind(0, staged_prev) : 0, true, SPS == 1);
+    step(f1, f0, s + 1, 1, wait_kind(1, staged_prev), false, true);
     s += 2;
-    for (int kt = 2; kt < KT; kt += 2, s += 2) {  // KT is even
-      step(f0, f1, s, kt, staged_prev && kt <= NST - 2 ? 2 : 1, false);
-      step(f1, f0, s + 1, kt + 1, staged_prev && kt + 1 <= NST - 2 ? 2 : 1, false);
+    for (int kt = 2; kt < KT; kt += 2, s += 2) {
+      step(f0, f1, s, kt, SPS == 1 ? wait_kind(kt, staged_prev) : 0, false, SPS == 1);
+      step(f1, f0, s + 1, kt + 1, wait_kind(kt + 1, staged_prev), false, true);
     }
     waitcnt_vm<LOADS>();
     staged_prev = epilogue(tile);
@@ -778,23 +755,52 @@ static int num_cus() {
   return cached[dev];
 }
 
+#ifndef FR_GEMM_RB_256x256
+#define FR_GEMM_RB_256x256 128
+#endif
+#ifndef FR_GEMM_RB_256x128
+#define FR_GEMM_RB_256x128 128
+#endif
+#ifndef FR_GEMM_RB_128x128
+#define FR_GEMM_RB_128x128 128
+#endif
+
+// Bytes of K per LDS row for a tile shape.
+template <int BN, int BM>
+constexpr int tile_rb() {
+  return BN == 256 && BM == 256 ? FR_GEMM_RB_256x256 : BN == 256 ? FR_GEMM_RB_256x128 : FR_GEMM_RB_128x128;
+}
+// Ring slots: the deepest ring that fits next to the scale buffers and the
+// epilogue staging (32 x 128 bytes per wave, or 32 x 64 where that buys a
+// needed slot).  The loads are latency-bound (about 1.3 us from issue to LDS on a
+// busy chip); at 64-byte rows this gives 4, 5 and 8 slots for the 256x256,
+// 256x128 and 128x128 tiles.
+template <int BN, int BM, int RB>
+constexpr int ring_slots() {
+  constexpr int stage = (BN + BM) * RB;
+  constexpr int wide = (160 * 1024 - 2 * 2048 - 4 * 32 * 128) / stage;
+  constexpr int narrow = (160 * 1024 - 2 * 2048 - 4 * 32 * 64) / stage;
+  // (at 64-byte rows a sixth 256x128 slot bought with narrow staging measured
+  // no faster, so narrow staging is taken only below three slots)
+  constexpr int n = wide >= 3 || narrow == wide ? wide : narrow;
+  constexpr int cap = 8 * kBK / RB;
+  return n > cap ? cap : n;
+}
+
 template <int BN, int BM, int OUT>
 static hipError_t launch_mfma(const GemmArgs& g, hipStream_t st) {
-  // LDS: ring of 64-byte K steps within 128 KB, plus 32 KB epilogue staging.
-  // The loads are latency-bound (about 1.3 us from issue to LDS on a busy
-  // chip), so the deepest ring that fits is used: 4, 5 and 8 steps for the
-  // 256x256, 256x128 and 128x128 tiles.
-  constexpr int NST = (128 * 1024) / ((BN + BM) * kBK) > 8 ? 8 : (128 * 1024) / ((BN + BM) * kBK);
+  constexpr int RB = tile_rb<BN, BM>();
+  constexpr int NSL = ring_slots<BN, BM, RB>();
   const int64_t nt = ((g.N + BN - 1) / BN) * ((g.M + BM - 1) / BM);
   const int64_t cus = num_cus();
-  // The ring runs NST steps ahead, which may only reach into the next tile:
+  // The ring runs NSL slots ahead, which may only reach into the next tile:
   // with fewer K steps per tile than that, give every tile its own workgroup.
   const int64_t kt = ((g.K + 2 * kBK - 1) / (2 * kBK)) * 2;
-  const unsigned grid = static_cast<unsigned>(nt < cus || kt < NST ? nt : cus);
+  const unsigned grid = static_cast<unsigned>(nt < cus || kt < NSL * (RB / kBK) ? nt : cus);
   if (g.K % (2 * kBK) == 0)
-    hipLaunchKernelGGL((gemm_fp8_mfma<BN, BM, NST, OUT, false>), dim3(grid), dim3(256), 0, st, g);
+    hipLaunchKernelGGL((gemm_fp8_mfma<BN, BM, NSL, RB, OUT, false>), dim3(grid), dim3(256), 0, st, g);
   else
-    hipLaunchKernelGGL((gemm_fp8_mfma<BN, BM, NST, OUT, true>), dim3(grid), dim3(256), 0, st, g);
+    hipLaunchKernelGGL((gemm_fp8_mfma<BN, BM, NSL, RB, OUT, true>), dim3(grid), dim3(256), 0, st, g);
   return hipGetLastError();
 }
 
