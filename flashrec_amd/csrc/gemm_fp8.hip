@@ -17,14 +17,18 @@
 //    matter as long as both operands use the same (lane group, byte) -> k
 //    assignment: lane l supplies row l%32 and bytes (l/32)*32 .. +31 of the
 //    64-byte K step, for both operands.
-//  * K is consumed in 64-byte steps through an NST-slot LDS ring filled by
-//    buffer_load ... lds (no VGPR staging; rows past M/N and the K tail read
-//    as zero through the buffer range check).  One barrier per step.
-//  * Fragments of step s+1 are read from LDS while the last MFMAs of step s
-//    run (register double buffering).
+//  * K is consumed in 64-byte MFMA steps from an LDS ring whose rows hold
+//    128 bytes of K (two steps per slot), filled by buffer_load ... lds (no
+//    VGPR staging; rows past M/N and the K tail read as zero through the
+//    buffer range check).  Each 1 KB load then covers 8 whole 128-byte
+//    lines, which the direct-to-LDS path moves much faster than 16 half
+//    lines.  One barrier per slot.
+//  * Fragments of step s+1 are read from LDS while the MFMAs of step s run
+//    (register double buffering).
 //  * Epilogue: scales applied in fp32, converted, transposed through a
-//    separate 8 KB-per-wave LDS staging area and written as full 256-byte
-//    row segments (16 lanes x 16 B), instead of scattered 8-byte pieces.
+//    per-wave LDS staging tile and written as whole 128- (or 64-) byte row
+//    segments through a buffer resource with scalar offsets, the passes
+//    software-pipelined.
 //  * Workgroup -> tile mapping is XCD aware: dispatch places workgroup i on
 //    XCD i % 8; tiles are renumbered so each XCD walks a contiguous, m-grouped
 //    range and its 32 CUs share weight/activation panels in their L2.
@@ -53,7 +57,7 @@ struct GemmArgs {
   int64_t M, N, K;
 };
 
-constexpr int kBK = 64;  // bytes of K per LDS step (one MFMA K step)
+constexpr int kBK = 64;  // bytes of K per MFMA step
 
 // LDS rows are 64 bytes (4 chunks of 16 B); chunk c of row r lives in slot
 // c ^ g(r) with g(r) = r2 | (r1 ^ r3) << 1 (r_i = bit i of r).  For the
@@ -287,10 +291,11 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
 
   // ---- direct-to-LDS loads.  One wave instruction fills 1 KB = RPI rows of
   // RB bytes; lane L lands in row L/CPR, chunk slot L%CPR, so it fetches the
-  // global chunk (L%CPR) ^ g(L/CPR).  Per-lane row offsets are kept for the tile being
-  // computed (cur) and the next one (nxt): the ring runs NST steps ahead, so
-  // the last NST steps of a tile load the first ones of the next.  Offsets of
-  // a tile past the end are out of range (loads return zeros, touch nothing).
+  // global chunk (L%CPR) ^ g(L/CPR).  Per-lane row offsets are kept for the
+  // tile being computed (cur) and the next one (nxt): the ring runs NSL slots
+  // ahead, so the last NSL slots of a tile load the first ones of the next.
+  // Offsets of a tile past the end are out of range (loads return zeros,
+  // touch nothing).
   // The swizzle depends on row bits 0-3.  A load covers 16 (RB = 64) or 8
   // (RB = 128) rows starting at a multiple of 16 or 8: in the second case
   // bit 3 of the row is the parity of the load's index l*4 + wave, i.e. of
