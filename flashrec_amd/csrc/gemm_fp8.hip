@@ -643,10 +643,15 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   static_assert(NSL >= 2, "ring of at least two slots");
   constexpr int NMF = FN * FM;                   // MFMAs per step
   constexpr int NRD = 2 * (FN + FM);             // 16-byte LDS reads per step
-  // Measured on the 4096-row gate_up and down shapes: these placements beat
-  // reads over the first half and loads from the first MFMA or from the half.
+  // Fragment reads over the first three quarters of the step's MFMAs, the
+  // refill loads over all of them.  Measured with 128-byte rows on the
+  // 4096-row gate_up, qkv and down shapes against reads over 1/2, 5/8, 7/8
+  // or all MFMAs and loads from 1/8, 1/4 or 1/2 on, or ending at 1/2 or
+  // 3/4: this placement was best or within 1 % on each (gate_up +4 % over
+  // loads from 1/4 on).
   constexpr int RDU = NMF * 3 / 4;  // MFMAs the fragment reads spread over
-  constexpr int LD0 = NMF / 4;      // first MFMA followed by a ring load
+  constexpr int LD0 = 0;            // first MFMA followed by a ring load
+  constexpr int LDE = NMF;          // loads spread over MFMAs LD0 .. LDE-1
   // Wait kinds: 0 none, 1 the slot's loads (the NSL-2 newer slots' loads may
   // be in flight), 2 the same with the previous tile's staged stores also
   // allowed in flight (they were issued after the loads waited for).  The
@@ -694,7 +699,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
       if (last) {
 #pragma unroll
         for (int l = 0; l < LOADS; ++l)
-          if (LD0 + l * (NMF - LD0) / LOADS == u) issue_one(slot, lq, nx, l);
+          if (LD0 + l * (LDE - LD0) / LOADS == u) issue_one(slot, lq, nx, l);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
