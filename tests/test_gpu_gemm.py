@@ -142,3 +142,18 @@ def test_gemm_multi_tile_edges(dev, m, n, k, out_dtype):
     got = out[rows].float()
     assert max_abs_rel(got, ref) < TOL
     assert torch.isfinite(out).all()
+
+
+@pytest.mark.parametrize("m,n,k", [(2048 + 37, 4096, 2064), (4096, 2048, 1088), (512, 12288, 2112)])
+def test_gemm_k_tail_multi_tile(dev, m, n, k):
+    """K not a multiple of the 128-byte ring rows (K % 128 = 16, 64, 64) on
+    shapes that give workgroups several tiles (256x256, 256x128 and the
+    single-round 256x128 path): the zero-filled tail of each tile's last slot
+    must not leak into the next tile's first slots."""
+    qa, sa, qw, sw = _operands(m, n, k, seed=k)
+    out = _run(dev, qa, sa, qw, sw).cpu()
+    g = torch.Generator().manual_seed(6)
+    rows = torch.cat([torch.randperm(m, generator=g)[:48], torch.arange(m - 16, m)])
+    ref = ops.fp8_scaled_mm(qa[rows], qw.t(), sa[rows], sw)
+    assert max_abs_rel(out[rows].float(), ref) < TOL
+    assert torch.isfinite(out).all()
