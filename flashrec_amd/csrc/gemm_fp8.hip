@@ -105,8 +105,8 @@ __device__ __forceinline__ void waitcnt_vm() {
 // tell plain LDS accesses from the ring's direct-to-LDS writes, so before each
 // one it would wait for vmcnt(0) -- all ring loads and every output store
 // issued so far.  These need no such wait (the scales landed long before, and
-// the staging area is never a direct-load target); the reads carry their own
-// lgkmcnt wait.
+// the staging area is never a direct-load target); their lgkmcnt waits are
+// explicit (lds_wait_all, the pass loop's wait).
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
 }
@@ -115,16 +115,6 @@ __device__ __forceinline__ void lds_write_b64(uint32_t a, uint32_t lo, uint32_t 
 }
 __device__ __forceinline__ void lds_write_b128(uint32_t a, u32x4 v) {
   asm volatile("ds_write_b128 %0, %1" ::"v"(a), "v"(v) : "memory");
-}
-// four 16-byte reads, then the wait for all of them
-__device__ __forceinline__ void lds_read4_b128(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3,
-                                               u32x4& r0, u32x4& r1, u32x4& r2, u32x4& r3) {
-  asm volatile(
-      "ds_read_b128 %0, %4\n\tds_read_b128 %1, %5\n\tds_read_b128 %2, %6\n\tds_read_b128 %3, %7\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
-      : "v"(a0), "v"(a1), "v"(a2), "v"(a3)
-      : "memory");
 }
 // Reads without their wait; lds_wait_all() then retires them all and, by
 // taking the registers as operands, keeps every use after it.
@@ -145,11 +135,6 @@ __device__ __forceinline__ void lds_wait_all(u32x4 (&v)[NV], float (&f)[NF]) {
   for (int i = 0; i < NV; ++i) asm volatile("" : "+v"(v[i]));
 #pragma unroll
   for (int i = 0; i < NF; ++i) asm volatile("" : "+v"(f[i]));
-}
-__device__ __forceinline__ float lds_read_f32(uint32_t a) {
-  float r;
-  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(a) : "memory");
-  return r;
 }
 
 // Lane id, computed where it is written (a volatile asm is never hoisted
