@@ -246,7 +246,10 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   constexpr int EB = OutT<OUT>::kBytes;
   // LDS: the slot ring, two 2 KB scale buffers, per-wave epilogue staging of
   // 32 rows x 128 bytes, or x 64 bytes where the wider staging does not fit
-  constexpr bool kNarrow = NSL * STAGE + 2 * 2048 + 4 * 32 * 128 > 160 * 1024;
+  // (narrow also when a wave's columns are not whole 128-byte staging rows:
+  // the 192-column tile with 16-bit outputs)
+  constexpr bool kNarrow =
+      NSL * STAGE + 2 * 2048 + 4 * 32 * 128 > 160 * 1024 || (BN / 2) % (128 / OutT<OUT>::kBytes) != 0;
   constexpr int SRB = kNarrow ? 64 : 128;  // staging row bytes
   constexpr int STG = 32 * SRB;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NSL * STAGE + 2 * 2048 + 4 * STG];
@@ -763,7 +766,7 @@ static int num_cus() {
 // Bytes of K per LDS row for a tile shape.
 template <int BN, int BM>
 constexpr int tile_rb() {
-  return BN == 256 && BM == 256 ? FR_GEMM_RB_256x256 : BN == 256 ? FR_GEMM_RB_256x128 : FR_GEMM_RB_128x128;
+  return BN == 256 && BM == 256 ? FR_GEMM_RB_256x256 : BN >= 192 ? FR_GEMM_RB_256x128 : FR_GEMM_RB_128x128;
 }
 // Ring slots: the deepest ring that fits next to the scale buffers and the
 // epilogue staging (32 x 128 bytes per wave, or 32 x 64 where that buys a
@@ -813,13 +816,24 @@ static hipError_t dispatch(const GemmArgs& g, hipStream_t st) {
                        dim3(256), 0, st, g);
     return hipGetLastError();
   }
-  // Tile choice: 256x256 when every CU gets a tile.  Otherwise 256x128 when
-  // that fills at least half the CUs in one round: measured at M=512,
-  // N=12288 (192 tiles), one round of 256x128 beats 1.5 rounds of 128x128.
+  // Tile choice: the shape with the least estimated time, rounds of tiles
+  // over the CUs (persistent workgroups: a partial round costs a full one)
+  // times a tile's MFMA work over its relative K-loop efficiency.  The
+  // efficiencies are measured TFLOP/s per tile shape on 4096-row shapes
+  // (256x256 1.0, 256x128 0.9, 192x128 0.85, 128x128 0.7).  E.g. M=4096,
+  // N=12288 takes 256x256 (3 rounds); N=2048 takes 256x128 (one round);
+  // M=512, N=12288 takes 192x128 (256 tiles: one round on every CU, where
+  // 256x128 leaves 64 CUs idle).
   const int64_t cus = num_cus();
   auto tiles = [&](int bn, int bm) __attribute__((always_inline)) { return ((g.N + bn - 1) / bn) * ((g.M + bm - 1) / bm); };
-  if (tiles(256, 256) >= cus) return launch_mfma<256, 256, OUT>(g, st);
-  if (2 * tiles(256, 128) >= cus) return launch_mfma<256, 128, OUT>(g, st);
+  auto cost = [&](int bn, int bm, double eff) __attribute__((always_inline)) {
+    return static_cast<double>((tiles(bn, bm) + cus - 1) / cus) * bn * bm / eff;
+  };
+  const double c256 = cost(256, 256, 1.0), c2561 = cost(256, 128, 0.9), c192 = cost(192, 128, 0.85),
+               c128 = cost(128, 128, 0.7);
+  if (c256 <= c2561 && c256 <= c192 && c256 <= c128) return launch_mfma<256, 256, OUT>(g, st);
+  if (c2561 <= c192 && c2561 <= c128) return launch_mfma<256, 128, OUT>(g, st);
+  if (c192 <= c128) return launch_mfma<192, 128, OUT>(g, st);
   return launch_mfma<128, 128, OUT>(g, st);
 }
 

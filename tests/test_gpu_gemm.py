@@ -157,3 +157,18 @@ def test_gemm_k_tail_multi_tile(dev, m, n, k):
     ref = ops.fp8_scaled_mm(qa[rows], qw.t(), sa[rows], sw)
     assert max_abs_rel(out[rows].float(), ref) < TOL
     assert torch.isfinite(out).all()
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("m,n,k", [(512, 12288, 2048), (512, 12200, 2048), (500, 12288, 1040)])
+def test_gemm_192_column_tiles(dev, m, n, k, out_dtype):
+    """The 192 x 128 tile (taken when it gives every CU one tile, e.g. 512
+    rows x 12288): full tiles, a partial last column tile, a partial last row
+    tile and a K tail."""
+    qa, sa, qw, sw = _operands(m, n, k, seed=n + k)
+    out = _run(dev, qa, sa, qw, sw, out_dtype=out_dtype).cpu()
+    g = torch.Generator().manual_seed(7)
+    rows = torch.cat([torch.randperm(m, generator=g)[:32], torch.arange(m - 16, m)])
+    ref = ops.fp8_scaled_mm(qa[rows], qw.t(), sa[rows], sw)
+    assert max_abs_rel(out[rows].float(), ref) < TOL
+    assert torch.isfinite(out).all()
