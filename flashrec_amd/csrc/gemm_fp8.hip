@@ -465,7 +465,9 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     // cg outer, covering CPP output columns (NQ groups u of 8: lane l holds
     // columns 8u + 4(l/32) .. +3 of its row l%32).  The converted outputs go
     // to the wave's staging tile (16-byte chunk c of row r at slot
-    // c ^ (r % CPRS)), are read back as 16 consecutive bytes per lane and
+    // c ^ ((r / RPL) % CPRS), RPL = staging rows per 256-byte bank line: a
+    // write of one column group by all 64 lanes then hits each bank at most
+    // twice), are read back as 16 consecutive bytes per lane and
     // stored as whole SRB-byte row segments.  Passes are software-pipelined:
     // pass t+1 is scaled and converted while pass t's reads are in flight.
     constexpr int CPP = SRB / EB;        // output columns per pass
@@ -473,6 +475,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     constexpr int NCG = WN / CPP;        // column groups per wave
     constexpr int NP = NCG * FM;         // passes
     constexpr int CPRS = SRB / 16;       // 16-byte chunks per staging row (= lanes per row on read-back)
+    constexpr int RPL = 256 / SRB;       // staging rows per 256-byte LDS bank line
     constexpr int RPR = 64 / CPRS;       // rows per read-back instruction
     constexpr int NR = 32 / RPR;         // read-backs (and stores) per pass
     static_assert(NP * NR == kStagedStores, "store count per tile");
@@ -492,7 +495,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
 #pragma unroll
     for (int rr = 0; rr < NR; ++rr) {
       const int r = rr * RPR + lx / CPRS;
-      ra[rr] = stg_base + r * SRB + (((lx % CPRS) ^ (r % CPRS)) << 4);
+      ra[rr] = stg_base + r * SRB + (((lx % CPRS) ^ ((r / RPL) % CPRS)) << 4);
     }
     // scales: sa of the wave's rows up front, sb per column group
     u32x4 sb4[NQ];
@@ -535,7 +538,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
 #pragma unroll
       for (int u = 0; u < NQ; ++u) {
         const int byte = (8 * u + h4) * EB;  // inside the staging row
-        const uint32_t ad = stg_base + row * SRB + ((((byte >> 4) ^ (row % CPRS))) << 4) + (byte & 15);
+        const uint32_t ad = stg_base + row * SRB + ((((byte >> 4) ^ ((row / RPL) % CPRS))) << 4) + (byte & 15);
         if constexpr (EB == 4) lds_write_b128(ad, pk[u]);
         else lds_write_b64(ad, pk[u][0], pk[u][1]);
       }
