@@ -188,6 +188,22 @@ def test_silu_and_mul_bf16(dev):
     assert_bf16_parity(out, ops.silu_and_mul(x))
 
 
+@pytest.mark.parametrize("scale", [1.0, 4.0, 20.0])
+def test_silu_wide_gate_range(dev, scale):
+    """Gates over a wide range (|g| up to ~80 at scale 20, where the
+    exponent's fp32 argument is least exact): the bf16 silu(g) * u and the
+    e4m3 codes match the reference composition (flip bar as elsewhere; none
+    were observed on these inputs)."""
+    from flashrec_amd.kernel.sglops import silu_and_mul
+    from flashrec_amd.kernel.silu_fp8 import silu_and_mul_per_token_quant_fp8
+
+    x = _bf16((256, 2 * 6144), seed=int(scale) + 40, scale=scale)
+    assert_bf16_parity(silu_and_mul(x.to(dev)), ops.silu_and_mul(x))
+    q, s = silu_and_mul_per_token_quant_fp8(x.to(dev))
+    q_ref, s_ref = ops.silu_and_mul_per_token_quant_fp8(x)
+    assert_fp8_parity(q, s, q_ref, s_ref)
+
+
 def test_empty_batch(dev):
     from flashrec_amd.kernel.sglops import per_token_quant_fp8
 
