@@ -342,6 +342,23 @@ __global__ __launch_bounds__(256, 2) void paged_attn_grouped_d128(AttnArgs a) {
   const int kh = static_cast<int>(item - group * a.Hk);
   const int64_t t0 = group * TOK;
   if (t0 >= a.T) return;
+  const int n = lane & 31;  // query column (and key row when loading)
+  const int h = lane >> 5;  // half: dims 64h .. 64h + 63
+  // this lane's query and key token: t0 + n / NREP (head kh * NREP + n % NREP).
+  // Its row bounds and query are fetched before the plan entry is examined,
+  // so those loads share one latency with it.
+  const int64_t tq = t0 + n / NREP;
+  const bool qok = tq < a.T;
+  const int32_t qlen = qok ? a.kv_len[tq] : 0;
+  const int32_t* ik = a.kv_indices + (qok ? a.kv_start[tq] : 0);
+  const int32_t* i0 = a.kv_indices + a.kv_start[t0];
+  u32x4 qb[8];
+  {
+    const uint16_t* qp = a.q + (qok ? tq : 0) * a.sqt + (kh * NREP + n % NREP) * a.sqh + 64 * h;
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      qb[s] = qok ? *reinterpret_cast<const u32x4*>(qp + 8 * s) : u32x4{0, 0, 0, 0};
+  }
   // A group without a shared 32-slot block is attended token by token on
   // the VALU: here, by this wave for its kv head, when the per-token
   // registers fit two waves per SIMD (NREP < 8); otherwise by
@@ -354,24 +371,9 @@ __global__ __launch_bounds__(256, 2) void paged_attn_grouped_d128(AttnArgs a) {
     return;
   }
   uint8_t* vs = lds + wave * (32 * kVRow);
-  const int n = lane & 31;  // query column (and key row when loading)
-  const int h = lane >> 5;  // half: dims 64h .. 64h + 63
-
-  // this lane's query: token t0 + n / NREP, head kh * NREP + n % NREP
-  const int64_t tq = t0 + n / NREP;
-  const bool qok = tq < a.T;
-  const int32_t qlen = qok ? a.kv_len[tq] : 0;
-  u32x4 qb[8];
-  {
-    const uint16_t* qp = a.q + (qok ? tq : 0) * a.sqt + (kh * NREP + n % NREP) * a.sqh + 64 * h;
-#pragma unroll
-    for (int s = 0; s < 8; ++s)
-      qb[s] = qok ? *reinterpret_cast<const u32x4*>(qp + 8 * s) : u32x4{0, 0, 0, 0};
-  }
 
   // ---- shared slot prefix of the group's tokens: from the plan, or found here
   const int32_t P32 = a.gp ? a.gp[group] : group_prefix32<TOK>(a, t0, lane);
-  const int32_t* i0 = a.kv_indices + a.kv_start[t0];
 
   // ---- running softmax state of this lane's query (the two halves hold the
   // same m; l and O are per half: O^T rows 32mt + 8(v/4) + 4h + v%4)
@@ -386,10 +388,7 @@ __global__ __launch_bounds__(256, 2) void paged_attn_grouped_d128(AttnArgs a) {
   // i0[32b + n] for every query; after that, row r holds position
   // P32 + j * NREP + r % NREP (j = b - nshared) of token t0 + r / NREP and
   // each query only sees its own token's rows.
-  const int64_t tk = t0 + n / NREP;
-  const bool tk_ok = tk < a.T;
-  const int32_t klen = tk_ok ? a.kv_len[tk] : 0;
-  const int32_t* ik = a.kv_indices + (tk_ok ? a.kv_start[tk] : 0);
+  const int32_t klen = qlen;
   int32_t rest = klen - P32;
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) rest = max(rest, __shfl_xor(rest, o, 64));
