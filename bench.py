@@ -304,6 +304,72 @@ def cpu_baseline(target_s: float = 3.0, runs: int = 3):
     }
 
 
+def cpu_decode_step_extrapolated():
+    """Config 4 on the host, as the baseline plan asks: one Qwen3-1.7B-shaped
+    decoder layer at 4096 rows through the reference's CPU path (the oracle's
+    restatement: RMSNorm->fp8, qkv / o / gate_up / down through
+    torch._scaled_mm as sglops.py:111-139 runs it, QK-norm + RoPE + fp8 KV
+    store, the bf16 gather + SDPA decode of flashinfer.py:380-431, SiLU->fp8),
+    x 28 layers, plus the fp8 SID lm_head and log_softmax."""
+    from oracle import ops
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    g = torch.Generator().manual_seed(4)
+    T, H, I, Hq, Hk, D, eps = 4096, 2048, 6144, 16, 8, 128, 1e-6
+    reqs, prefix = 8, 128
+
+    def wq(n, k):
+        return ops.quantize_weight_fp8((0.02 * torch.randn(n, k, generator=g)).to(torch.bfloat16))
+
+    (wqkv, sqkv), (wo, so), (wgu, sgu), (wd, sd) = wq((Hq + 2 * Hk) * D, H), wq(H, Hq * D), wq(2 * I, H), wq(H, I)
+    nw = [(1 + 0.1 * torch.randn(n, generator=g)).to(torch.bfloat16) for n in (H, H, D, D)]
+    slots = 1 + reqs * prefix + T
+    kc = torch.randn(slots, Hk, D, generator=g).to(torch.float8_e4m3fn)
+    vc = torch.randn(slots, Hk, D, generator=g).to(torch.float8_e4m3fn)
+    pre = 1 + torch.arange(reqs * prefix, dtype=torch.int64).view(reqs, prefix)
+    own = 1 + reqs * prefix + torch.arange(T, dtype=torch.int64)
+    rows = torch.cat([pre.repeat_interleave(T // reqs, 0), own[:, None]], 1)  # [T, prefix + 1]
+    kv_indices = rows.reshape(-1).to(torch.int32)
+    kv_indptr = torch.arange(T + 1, dtype=torch.int64) * (prefix + 1)
+    positions = torch.full((T,), prefix, dtype=torch.int64)
+    cache = ops.cos_sin_cache(D, 4096, 1e6)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    residual = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    lm_w = (0.02 * torch.randn(8192, H, generator=g)).to(torch.bfloat16)
+
+    def layer():
+        t0 = time.perf_counter()
+        q8, s8, res = ops.fused_add_rmsnorm_per_token_quant_fp8(x, residual, nw[0], eps)
+        qkv = ops.fp8_scaled_mm_torch_cpu(q8, wqkv.t(), s8, sqkv, torch.bfloat16).view(T, Hq + 2 * Hk, D)
+        q = ops.qk_norm_rope_store_fp8(qkv[:, :Hq], qkv[:, Hq:Hq + Hk], qkv[:, Hq + Hk:], positions, own,
+                                       nw[2], nw[3], eps, cache, kc, vc)
+        o = ops.sdpa_reference_style(q, kc, vc, kv_indices, kv_indptr)
+        o8, os8 = ops.per_token_quant_fp8(o.reshape(T, Hq * D))
+        h = ops.fp8_scaled_mm_torch_cpu(o8, wo.t(), os8, so, torch.bfloat16)
+        q8, s8, res = ops.fused_add_rmsnorm_per_token_quant_fp8(h, res, nw[1], eps)
+        gu = ops.fp8_scaled_mm_torch_cpu(q8, wgu.t(), s8, sgu, torch.bfloat16)
+        y8, ys = ops.silu_and_mul_per_token_quant_fp8(gu)
+        ops.fp8_scaled_mm_torch_cpu(y8, wd.t(), ys, sd, torch.bfloat16)
+        return time.perf_counter() - t0
+
+    def head():
+        t0 = time.perf_counter()
+        lw8, lws = ops.quantize_weight_fp8(lm_w)
+        a8, a_s = ops.per_token_quant_fp8(residual)
+        logits = ops.fp8_scaled_mm_torch_cpu(a8, lw8.t(), a_s, lws, torch.float32)
+        torch.log_softmax(logits.float(), dim=-1)
+        return time.perf_counter() - t0
+
+    # the baseline plan's protocol: one warm-up, then the median of 5 runs
+    layer_s = sorted([layer() for _ in range(6)][1:])[2]
+    head_s = sorted([head() for _ in range(6)][1:])[2]
+    return {"seconds_extrapolated": round(28 * layer_s + head_s, 3), "layer_s": round(layer_s, 3),
+            "lm_head_s": round(head_s, 3), "layers": 28, "cores": torch.get_num_threads(),
+            "runs": "median of 5 after 1 warm-up",
+            "note": "one decoder layer on the host counted 28 times, plus the fp8 SID lm_head; the "
+                    "trie mask / beam tail is not included"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -399,6 +465,8 @@ def main() -> int:
         result["extra"] = extra
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline()
+        if not args.quick:
+            result["cpu_baseline"]["config4_decode_step"] = cpu_decode_step_extrapolated()
     print(json.dumps(result), flush=True)
     return 0
 
