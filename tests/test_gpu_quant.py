@@ -169,7 +169,7 @@ def test_fused_add_rmsnorm_bf16_inplace(dev):
     assert_bf16_parity(y, y_ref)
 
 
-@pytest.mark.parametrize("m,two_d", [(12, 96), (64, 12288), (4096, 12288), (5, 100), (3, 20000)])
+@pytest.mark.parametrize("m,two_d", [(12, 96), (64, 12288), (4096, 12288), (5, 100), (3, 20000), (33, 4096), (7, 16384)])
 def test_silu_quant(dev, m, two_d):
     from flashrec_amd.kernel.silu_fp8 import silu_and_mul_per_token_quant_fp8
 
