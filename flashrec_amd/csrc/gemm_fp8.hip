@@ -614,15 +614,16 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
 
   // ---- main loop.  Step s (tile s / KT, K step kt = s % KT; ring slot
   // q = s / SPS, step s % SPS inside it) holds its fragments in `cur` and
-  // reads step s+1's into `nxt`.  The last step of a slot first waits for
-  // the next slot (own loads, then everyone's through the barrier, which also
-  // retires every wave's reads of slot q, whose steps are all in registers
-  // by then), refills slot q with slot q+NSL, and spreads those loads over
-  // its MFMAs.  Each MFMA is followed by its share of the next step's
-  // fragment reads (over the first three quarters) and of the refill loads
-  // (from the first quarter on), so the LDS reads of the CU's four waves
-  // overlap the matrix work instead of stalling the next step.  Past the end
-  // the ring loads zeros and the last fragment read is discarded.
+  // reads step s+1's into `nxt`.  The last step of a slot opens with a
+  // barrier that retires every wave's reads of slot q (whose steps are all in
+  // registers by then), refills slot q with slot q+NSL, spreading those loads
+  // over its MFMAs, and a few MFMAs in waits for the next slot (own loads,
+  // then everyone's through a second barrier) before reading from it.  Each
+  // MFMA is followed by its share of the next step's fragment reads (over
+  // three quarters of the MFMAs that follow the wait) and of the refill
+  // loads, so the LDS reads of the CU's four waves overlap the matrix work
+  // instead of stalling the next step.  Past the end the ring loads zeros
+  // and the last fragment read is discarded.
   //
   // vmcnt retires loads and stores in issue order, so a plain load wait issued
   // while the epilogue's stores are in flight would also wait for them.
@@ -648,16 +649,39 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   // allowed in flight (they were issued after the loads waited for).  The
   // count is capped at vmcnt's 63: a smaller count only waits for the
   // oldest few stores as well (conservative).
-  constexpr int kAdjN = (NSL - 2) * LOADS + kStagedStores < 63 ? (NSL - 2) * LOADS + kStagedStores : 63;
+  // The slot-final step opens with a barrier (every wave is done reading the
+  // slot, so its refill may start) and waits for the next slot only at MFMA
+  // MW, its fragment reads following from there: the newest refill loads get
+  // MW MFMAs more time to land.  Measured with MW at 1/4, 3/8, 1/2, 5/8 and 3/4
+  // of the step on the 4096-row gate_up, qkv, down and o shapes, M = 512 and
+  // fp32 outputs: 3/8 best or within 1 % on each, 2-7 % over waiting at the
+  // start (0 restores that).
+#ifndef FR_GEMM_MIDW
+#define FR_GEMM_MIDW 3
+#endif
+  constexpr int MW = FR_GEMM_MIDW * NMF / 8;
+  // refill loads of the same step issued before that point
+  constexpr int kEarly = [] {
+    int n = 0;
+    for (int l = 0; l < LOADS; ++l)
+      if (LD0 + l * (LDE - LD0) / LOADS < MW) ++n;
+    return n;
+  }();
+  constexpr int kWait1 = (NSL - 2) * LOADS + kEarly;
+  constexpr int kAdjN = kWait1 + kStagedStores < 63 ? kWait1 + kStagedStores : 63;
   auto step = [&](Frags& cur, Frags& nxt, int64_t s, int kt, int wait, bool first, bool last)
       __attribute__((always_inline)) {
     __builtin_amdgcn_sched_barrier(0);
-    if (last) {
+    auto slot_wait = [&]() __attribute__((always_inline)) {
       if (wait == 2)
         waitcnt_vm<kAdjN>();
       else if (wait != 0)
-        waitcnt_vm<(NSL - 2) * LOADS>();
+        waitcnt_vm<kWait1>();
       lds_barrier();
+    };
+    if (last) {
+      if (MW == 0) slot_wait();
+      else lds_barrier();
     }
     const int lq0 = kt / SPS + NSL;
     const int lq = lq0 < KS ? lq0 : lq0 - KS;
@@ -673,17 +697,32 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     // it has MFMAs to issue.
 #pragma unroll
     for (int u = 0; u < NMF; ++u) {
+      // reads of a slot-final step start at MFMA R0 (after the wait)
+      const int R0 = last ? MW : 0;
+      const int RU = last && MW > 0 ? (NMF - MW) * 3 / 4 : RDU;
+      if (last && MW > 0 && u == MW) {
+        slot_wait();
+        if constexpr (kOneB) {
+          // weight blocks whose last MFMA is already issued
+#pragma unroll
+          for (int i = 0; i < FN; ++i)
+            if (i * FM + FM - 1 < MW) {
+              read_one(nxt, nslot, nsub, 2 * i);
+              read_one(nxt, nslot, nsub, 2 * i + 1);
+            }
+        }
+      }
       if constexpr (kOneB) {
 #pragma unroll
         for (int r = 0; r < 2 * FM; ++r)
-          if (r * RDU / (2 * FM) == u) read_one(nxt, nslot, nsub, 2 * FN + r);
+          if (R0 + r * RU / (2 * FM) == u) read_one(nxt, nslot, nsub, 2 * FN + r);
       } else {
 #pragma unroll
         for (int r = 0; r < NRD; ++r)
-          if (r * RDU / NRD == u) read_one(nxt, nslot, nsub, r);
+          if (R0 + r * RU / NRD == u) read_one(nxt, nslot, nsub, r);
       }
       mfma_one(cur, u / FM, u % FM, first);
-      if (kOneB && u % FM == FM - 1) {
+      if (kOneB && u % FM == FM - 1 && !(last && MW > 0 && u < MW)) {
         read_one(nxt, nslot, nsub, 2 * (u / FM));
         read_one(nxt, nslot, nsub, 2 * (u / FM) + 1);
       }
