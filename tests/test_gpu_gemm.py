@@ -172,3 +172,28 @@ def test_gemm_192_column_tiles(dev, m, n, k, out_dtype):
     ref = ops.fp8_scaled_mm(qa[rows], qw.t(), sa[rows], sw)
     assert max_abs_rel(out[rows].float(), ref) < TOL
     assert torch.isfinite(out).all()
+
+
+@pytest.mark.parametrize("m,n,k,out_dtype", [
+    (4100, 136, 2064, torch.bfloat16),   # narrow N, K tail, ragged M
+    (1023, 2048, 1040, torch.float16),
+    (500, 12200, 256, torch.bfloat16),   # 192-column tiles, ragged N
+    (2048, 1000, 6144, torch.float32),
+    (64, 4096, 2048, torch.bfloat16),
+    (7, 48, 16, torch.float32),
+])
+def test_gemm_integer_exact_pow2_scales(dev, m, n, k, out_dtype):
+    """Small-integer operands with power-of-two row/column scales: every product,
+    sum and scaling step is exact in fp32, so the output must equal the exact
+    result rounded once to the output type, for every tile shape and dtype."""
+    g = torch.Generator().manual_seed(m * 7 + n + k)
+    a = torch.randint(-3, 4, (m, k), generator=g).double()
+    w = torch.randint(-3, 4, (n, k), generator=g).double()
+    sa = torch.exp2(torch.randint(-6, 2, (m, 1), generator=g).double())
+    sw = torch.exp2(torch.randint(-6, 2, (n,), generator=g).double())
+    if out_dtype == torch.float16:
+        sa = sa * 2.0 ** -6  # keep |out| inside fp16's range
+    qa, qw = a.float().to(torch.float8_e4m3fn), w.float().to(torch.float8_e4m3fn)
+    out = _run(dev, qa, sa.float(), qw, sw.float(), out_dtype=out_dtype)
+    ref = ((a @ w.t()) * sa * sw[None, :]).to(out_dtype)
+    assert torch.equal(out.cpu(), ref)
