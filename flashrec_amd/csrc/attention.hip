@@ -309,7 +309,7 @@ __global__ __launch_bounds__(256) void attn_group_plan(AttnArgs a, int32_t* gp, 
 // The keys past the shared prefix run through the same block with each
 // token's own keys (NREP per token per block) and every query masked to its
 // own token's keys.  A shared 128-slot prefix is thus read and multiplied
-// once for all 32 queries (config-4 decode: 44 us a layer for 4096 beams,
+// once for all 32 queries (config-4 decode, 4096 beams: 25-29 us a layer,
 // against 189 us token by token).
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
