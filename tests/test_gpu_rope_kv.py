@@ -3,7 +3,7 @@
 import pytest
 import torch
 
-from helpers import assert_bf16_parity, assert_rope_parity, code_flip_stats, codes
+from helpers import assert_rope_parity, code_flip_stats, codes
 from oracle import inputs, ops
 
 pytestmark = pytest.mark.gpu
