@@ -39,11 +39,11 @@ SIGNATURES = {
     "fr_abi_version": [],
     "fr_per_token_quant_fp8": [_P, _I32, _I64, _I64, _I64, _P, _P, _P],
     "fr_quantize_weight_fp8": [_P, _I32, _I64, _I64, _I64, _P, _P, _P],
-    "fr_rms_quant_fp8": [_P, _I64, _P, _I64, _P, _I64, _I64, _F32, _P, _P, _P],
-    "fr_rmsnorm": [_P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _F32, _P],
-    "fr_silu_quant_fp8": [_P, _I64, _I64, _I64, _P, _P, _P],
-    "fr_silu_and_mul": [_P, _I64, _P, _I64, _I64, _I64, _P],
-    "fr_fp8_scaled_mm": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I32, _P],
+    "fr_rms_quant_fp8": [_P, _I32, _I64, _P, _I64, _P, _I64, _I64, _F32, _P, _P, _P],
+    "fr_rmsnorm": [_P, _I32, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _F32, _P],
+    "fr_silu_quant_fp8": [_P, _I32, _I64, _I64, _I64, _P, _P, _P],
+    "fr_silu_and_mul": [_P, _I32, _I64, _P, _I64, _I64, _I64, _P],
+    "fr_fp8_scaled_mm": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I32, _P],
     "fr_qk_norm_rope_store_fp8": [
         _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,  # q, k, v + strides
         _P, _P, _P, _P, _F32, _P, _I64,  # pos, loc, qw, kw, eps, cos_sin, rows
@@ -52,6 +52,13 @@ SIGNATURES = {
     ],
     "fr_rope_inplace": [_P, _I64, _I64, _P, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _P],
     "fr_store_kv_fp8": [_P, _I64, _P, _I64, _I32, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _P],
+    "fr_store_kv_bf16": [_P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _P],
+    "fr_rope_store_kv_bf16": [
+        _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,  # q, k, v + strides
+        _P, _P, _P, _I64,  # positions, loc, cos_sin, rows
+        _P, _I64, _I64, _P, _I64, _I64, _I64,  # caches + strides, num_slots
+        _I64, _I64, _I64, _I64, _P,  # T, Hq, Hk, D, stream
+    ],
     "fr_log_softmax_f32": [_P, _I64, _P, _I64, _I64, _I64, _P],
     "fr_genrec_scratch_bytes": [_I64, _I64, _I64],
     "fr_genrec_mask_topk_expand": [

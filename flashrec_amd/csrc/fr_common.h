@@ -75,11 +75,22 @@ template <>
 struct Elem<FR_DTYPE_BF16> {
   using T = uint16_t;
   static __device__ __forceinline__ float load(const T* p) { return bf16_to_f32(*p); }
+  // round to this dtype (RNE) and the rounded value's bit pattern
+  static __device__ __forceinline__ float round(float x) { return round_bf16(x); }
+  static __device__ __forceinline__ uint16_t bits(float x) {
+    return static_cast<uint16_t>(pack_bf16x2(x, 0.0f) & 0xFFFFu);
+  }
 };
 template <>
 struct Elem<FR_DTYPE_FP16> {
   using T = uint16_t;
   static __device__ __forceinline__ float load(const T* p) { return fp16_to_f32(*p); }
+  static __device__ __forceinline__ float round(float x) {
+    return static_cast<float>(static_cast<_Float16>(x));
+  }
+  static __device__ __forceinline__ uint16_t bits(float x) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+  }
 };
 template <>
 struct Elem<FR_DTYPE_FP32> {

@@ -886,7 +886,7 @@ using namespace fr;
 extern "C" int fr_fp8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
                                 const float* scale_a, int64_t scale_a_numel,
                                 const float* scale_b, int64_t scale_b_numel, const void* bias,
-                                void* out, int64_t ldo, int64_t M, int64_t N, int64_t K,
+                                int64_t bias_numel, void* out, int64_t ldo, int64_t M, int64_t N, int64_t K,
                                 int out_dtype, void* stream) {
   if (M < 0 || N < 0 || K < 0) return FR_EINVAL;
   if (M == 0 || N == 0) return FR_OK;
@@ -894,6 +894,7 @@ extern "C" int fr_fp8_scaled_mm(const void* a, int64_t lda, const void* b, int64
   if (lda < K || ldb < K || ldo < N) return FR_EINVAL;
   if (!(scale_a_numel == 1 || scale_a_numel == M)) return FR_EINVAL;
   if (!(scale_b_numel == 1 || scale_b_numel == N)) return FR_EINVAL;
+  if (bias && bias_numel != N) return FR_EINVAL;  // the epilogue reads bias[0..N)
   if (M * N > (int64_t)0x7FFFFFFF * 256) return FR_EUNSUPPORTED;
   GemmArgs g{};
   g.a = static_cast<const uint8_t*>(a);

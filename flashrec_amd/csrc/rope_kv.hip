@@ -58,16 +58,23 @@ __device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
 // head, HPW / 4 heads per lane, 8 contiguous elements (16 bytes) per lane per
 // head.  All of a wave's loads are issued before any arithmetic so each wave
 // keeps HPW / 4 KB in flight.
-// FUSED: norm + rope + KV store; otherwise plain RoPE of q and k in place
-// (python/flashrec/kernel/sglops.py:64-81, apply_rope_inplace).
-template <bool FUSED, int HPW>
+// MODE kRope: RoPE of q and k in place (python/flashrec/kernel/sglops.py:64-81,
+// apply_rope_inplace); kNormRopeFp8: per-head norm + RoPE, q in place, K/V
+// as e4m3 into the pool (the fused op); kRopeBf16: RoPE of q and k in place
+// plus K/V rows copied into a bf16 pool (sglops.py:154-204,
+// apply_rope_and_store_kv with matching dtypes).
+enum RopeMode { kRope = 0, kNormRopeFp8 = 1, kRopeBf16 = 2 };
+
+template <int MODE, int HPW>
 __global__ __launch_bounds__(256) void qk_rope_kv_d128(RopeArgs a) {
+  constexpr bool FUSED = MODE == kNormRopeFp8;  // per-head norm
+  constexpr bool STORE = MODE != kRope;         // K/V go to the pool
   constexpr int R = HPW / 4;  // heads per lane
   const int lane = threadIdx.x & 63;
   const int64_t item =
       static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int qg = a.Hq / HPW, kg = a.Hk / HPW;
-  const int per_tok = FUSED ? qg + 2 * kg : qg + kg;
+  const int per_tok = STORE ? qg + 2 * kg : qg + kg;
   const int64_t t = item / per_tok;
   if (t >= a.T) return;
   const int g = static_cast<int>(item - t * per_tok);
@@ -75,10 +82,10 @@ __global__ __launch_bounds__(256) void qk_rope_kv_d128(RopeArgs a) {
   const int j = lane & 15;   // 8-element chunk inside the head
   const int e0 = j * 8;
 
-  const int64_t slot = FUSED ? a.loc[t] : 0;
+  const int64_t slot = STORE ? a.loc[t] : 0;
   const bool slot_ok = slot >= 0 && slot < a.num_slots;
 
-  if (FUSED && g >= qg + kg) {  // V: straight e4m3 conversion into the slot
+  if (STORE && g >= qg + kg) {  // V: e4m3 conversion or bf16 copy into the slot
     if (!slot_ok) return;
     const int h0 = (g - qg - kg) * HPW + hs;
     u32x4 xv[R];
@@ -87,6 +94,12 @@ __global__ __launch_bounds__(256) void qk_rope_kv_d128(RopeArgs a) {
       xv[r] = ldnt(reinterpret_cast<const u32x4*>(a.v + t * a.svt + (h0 + 4 * r) * a.svh + e0));
 #pragma unroll
     for (int r = 0; r < R; ++r) {
+      if (MODE == kRopeBf16) {
+        stnt(reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(a.vc) + slot * a.scvp +
+                                      (h0 + 4 * r) * a.scvh + e0),
+             xv[r]);
+        continue;
+      }
       float x[8];
       unpack8(xv[r], x);
       u32x2 o;
@@ -163,6 +176,8 @@ __global__ __launch_bounds__(256) void qk_rope_kv_d128(RopeArgs a) {
       const u32x4 o = yb;
       uint16_t* dst = is_q ? a.q + t * a.sqt + h * a.sqh : const_cast<uint16_t*>(a.k + t * a.skt + h * a.skh);
       stnt(reinterpret_cast<u32x4*>(dst + e0), o);
+      if (MODE == kRopeBf16 && !is_q && slot_ok)
+        stnt(reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(a.kc) + slot * a.sckp + h * a.sckh + e0), o);
     } else if (slot_ok) {
       float y[8];
       unpack8(yb, y);
@@ -176,22 +191,30 @@ __global__ __launch_bounds__(256) void qk_rope_kv_d128(RopeArgs a) {
 
 // Any even D <= 128, any head counts / element alignment: one wave per
 // (token, head); lane i < D/2 owns the rotate-half pair (i, i + D/2).
-template <bool FUSED>
+template <int MODE>
 __global__ __launch_bounds__(256) void qk_rope_kv_generic(RopeArgs a) {
+  constexpr bool FUSED = MODE == kNormRopeFp8;
+  constexpr bool STORE = MODE != kRope;
   const int lane = threadIdx.x & 63;
   const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  const int per_tok = FUSED ? a.Hq + 2 * a.Hk : a.Hq + a.Hk;
+  const int per_tok = STORE ? a.Hq + 2 * a.Hk : a.Hq + a.Hk;
   const int64_t t = item / per_tok;
   if (t >= a.T) return;
   const int hh = static_cast<int>(item - t * per_tok);
   const int half = a.D >> 1;
   const bool active = lane < half;
-  const int64_t slot = FUSED ? a.loc[t] : 0;
+  const int64_t slot = STORE ? a.loc[t] : 0;
   const bool slot_ok = slot >= 0 && slot < a.num_slots;
-  if (FUSED && hh >= a.Hq + a.Hk) {
+  if (STORE && hh >= a.Hq + a.Hk) {
     const int h = hh - a.Hq - a.Hk;
     if (!slot_ok || !active) return;
     const uint16_t* src = a.v + t * a.svt + h * a.svh;
+    if (MODE == kRopeBf16) {
+      uint16_t* dst = reinterpret_cast<uint16_t*>(a.vc) + slot * a.scvp + h * a.scvh;
+      dst[lane] = src[lane];
+      dst[lane + half] = src[lane + half];
+      return;
+    }
     uint8_t* dst = a.vc + slot * a.scvp + h * a.scvh;
     dst[lane] = static_cast<uint8_t>(e4m3_torch_byte(bf16_to_f32(src[lane])));
     dst[lane + half] = static_cast<uint8_t>(e4m3_torch_byte(bf16_to_f32(src[lane + half])));
@@ -220,8 +243,15 @@ __global__ __launch_bounds__(256) void qk_rope_kv_generic(RopeArgs a) {
   const float y2 = round_bf16(n2 * c + n1 * s);
   if (is_q || !FUSED) {
     uint16_t* dq = is_q ? a.q + t * a.sqt + h * a.sqh : const_cast<uint16_t*>(src);
-    dq[lane] = static_cast<uint16_t>(pack_bf16x2(y1, 0.f) & 0xFFFFu);
-    dq[lane + half] = static_cast<uint16_t>(pack_bf16x2(y2, 0.f) & 0xFFFFu);
+    const uint16_t b1 = static_cast<uint16_t>(pack_bf16x2(y1, 0.f) & 0xFFFFu);
+    const uint16_t b2 = static_cast<uint16_t>(pack_bf16x2(y2, 0.f) & 0xFFFFu);
+    dq[lane] = b1;
+    dq[lane + half] = b2;
+    if (MODE == kRopeBf16 && !is_q && slot_ok) {
+      uint16_t* dk = reinterpret_cast<uint16_t*>(a.kc) + slot * a.sckp + h * a.sckh;
+      dk[lane] = b1;
+      dk[lane + half] = b2;
+    }
   } else if (slot_ok) {
     uint8_t* dst = a.kc + slot * a.sckp + h * a.sckh;
     dst[lane] = static_cast<uint8_t>(e4m3_torch_byte(y1));
@@ -268,6 +298,31 @@ __global__ __launch_bounds__(256) void store_kv_kernel(const void* k, int64_t sk
       dst[c] = src[c];
     }
   }
+}
+
+// bf16 K/V rows -> a bf16 pool (plain row copy to loc[t]); 16-byte pieces
+// when every row and stride allows it.
+__global__ __launch_bounds__(256) void store_kv_bf16_kernel(const uint16_t* k, int64_t skt,
+                                                            const uint16_t* v, int64_t svt,
+                                                            const int64_t* loc, uint16_t* kc,
+                                                            int64_t sck, uint16_t* vc, int64_t scv,
+                                                            int64_t num_slots, int64_t T,
+                                                            int64_t row_dim, bool vec) {
+  const int64_t per_row = vec ? row_dim / 8 : row_dim;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= 2 * T * per_row) return;
+  const int which = static_cast<int>(idx / (T * per_row));  // 0 = K, 1 = V
+  const int64_t r = idx - which * T * per_row;
+  const int64_t t = r / per_row;
+  const int64_t c = r - t * per_row;
+  const int64_t slot = loc[t];
+  if (slot < 0 || slot >= num_slots) return;
+  const uint16_t* src = (which ? v : k) + t * (which ? svt : skt);
+  uint16_t* dst = (which ? vc : kc) + slot * (which ? scv : sck);
+  if (vec)
+    *reinterpret_cast<u32x4*>(dst + c * 8) = *reinterpret_cast<const u32x4*>(src + c * 8);
+  else
+    dst[c] = src[c];
 }
 
 }  // namespace fr
@@ -321,15 +376,15 @@ int fr_qk_norm_rope_store_fp8(void* q, int64_t sqt, int64_t sqh, const void* k, 
                     sckh % 8 == 0 && scvp % 8 == 0 && scvh % 8 == 0;
   if (fast && Hq % 8 == 0 && Hk % 8 == 0) {
     const int64_t items = T * (Hq / 8 + 2 * (Hk / 8));
-    hipLaunchKernelGGL((qk_rope_kv_d128<true, 8>), dim3(static_cast<unsigned>((items + 3) / 4)),
+    hipLaunchKernelGGL((qk_rope_kv_d128<kNormRopeFp8, 8>), dim3(static_cast<unsigned>((items + 3) / 4)),
                        dim3(256), 0, st, a);
   } else if (fast) {
     const int64_t items = T * (Hq / 4 + 2 * (Hk / 4));
-    hipLaunchKernelGGL((qk_rope_kv_d128<true, 4>), dim3(static_cast<unsigned>((items + 3) / 4)),
+    hipLaunchKernelGGL((qk_rope_kv_d128<kNormRopeFp8, 4>), dim3(static_cast<unsigned>((items + 3) / 4)),
                        dim3(256), 0, st, a);
   } else {
     const int64_t items = T * (Hq + 2 * Hk);
-    hipLaunchKernelGGL(qk_rope_kv_generic<true>, dim3(static_cast<unsigned>((items + 3) / 4)), dim3(256),
+    hipLaunchKernelGGL(qk_rope_kv_generic<kNormRopeFp8>, dim3(static_cast<unsigned>((items + 3) / 4)), dim3(256),
                        0, st, a);
   }
   return hipGetLastError() == hipSuccess ? FR_OK : FR_ELAUNCH;
@@ -362,11 +417,11 @@ int fr_rope_inplace(void* q, int64_t sqt, int64_t sqh, void* k, int64_t skt, int
                     al(cos_sin_cache, 16);
   if (fast) {
     const int64_t items = T * (Hq / 4 + Hk / 4);
-    hipLaunchKernelGGL((qk_rope_kv_d128<false, 4>), dim3(static_cast<unsigned>((items + 3) / 4)),
+    hipLaunchKernelGGL((qk_rope_kv_d128<kRope, 4>), dim3(static_cast<unsigned>((items + 3) / 4)),
                        dim3(256), 0, st, a);
   } else {
     const int64_t items = T * (Hq + Hk);
-    hipLaunchKernelGGL(qk_rope_kv_generic<false>, dim3(static_cast<unsigned>((items + 3) / 4)),
+    hipLaunchKernelGGL(qk_rope_kv_generic<kRope>, dim3(static_cast<unsigned>((items + 3) / 4)),
                        dim3(256), 0, st, a);
   }
   return hipGetLastError() == hipSuccess ? FR_OK : FR_ELAUNCH;
@@ -395,6 +450,72 @@ int fr_store_kv_fp8(const void* k, int64_t skt, const void* v, int64_t svt, int 
   else
     hipLaunchKernelGGL(store_kv_kernel<false>, grid, dim3(256), 0, st, k, skt, v, svt, loc, kc, sck,
                        vc, scv, num_slots, T, row_dim, vec);
+  return hipGetLastError() == hipSuccess ? FR_OK : FR_ELAUNCH;
+}
+
+int fr_store_kv_bf16(const void* k, int64_t skt, const void* v, int64_t svt, const int64_t* loc,
+                     void* k_cache, int64_t sck, void* v_cache, int64_t scv, int64_t num_slots,
+                     int64_t T, int64_t row_dim, void* stream) {
+  if (T < 0 || row_dim < 0) return FR_EINVAL;
+  if (T == 0 || row_dim == 0) return FR_OK;
+  if (!k || !v || !loc || !k_cache || !v_cache) return FR_EINVAL;
+  auto al = [](const void* p, unsigned m) { return (reinterpret_cast<uintptr_t>(p) & (m - 1)) == 0; };
+  const bool vec = row_dim % 8 == 0 && skt % 8 == 0 && svt % 8 == 0 && sck % 8 == 0 &&
+                   scv % 8 == 0 && al(k, 16) && al(v, 16) && al(k_cache, 16) && al(v_cache, 16);
+  const int64_t per_row = vec ? row_dim / 8 : row_dim;
+  const int64_t total = 2 * T * per_row;
+  hipLaunchKernelGGL(store_kv_bf16_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(k), skt,
+                     static_cast<const uint16_t*>(v), svt, loc, static_cast<uint16_t*>(k_cache), sck,
+                     static_cast<uint16_t*>(v_cache), scv, num_slots, T, row_dim, vec);
+  return hipGetLastError() == hipSuccess ? FR_OK : FR_ELAUNCH;
+}
+
+int fr_rope_store_kv_bf16(void* q, int64_t sqt, int64_t sqh, void* k, int64_t skt, int64_t skh,
+                          const void* v, int64_t svt, int64_t svh, const int64_t* positions,
+                          const int64_t* loc, const float* cos_sin_cache, int64_t cache_rows,
+                          void* k_cache, int64_t sckp, int64_t sckh, void* v_cache, int64_t scvp,
+                          int64_t scvh, int64_t num_slots, int64_t T, int64_t Hq, int64_t Hk,
+                          int64_t D, void* stream) {
+  if (T < 0 || Hq < 0 || Hk < 0) return FR_EINVAL;
+  if (D <= 0 || D > 128 || (D & 1)) return FR_EUNSUPPORTED;
+  if (T == 0) return FR_OK;
+  if (!q || !k || !v || !positions || !loc || !cos_sin_cache || !k_cache || !v_cache) return FR_EINVAL;
+  RopeArgs a{};
+  a.q = static_cast<uint16_t*>(q);
+  a.sqt = sqt; a.sqh = sqh;
+  a.k = static_cast<const uint16_t*>(k);
+  a.skt = skt; a.skh = skh;
+  a.v = static_cast<const uint16_t*>(v);
+  a.svt = svt; a.svh = svh;
+  a.pos = positions;
+  a.loc = loc;
+  a.cs = cos_sin_cache;
+  a.cs_rows = cache_rows;
+  a.kc = static_cast<uint8_t*>(k_cache);
+  a.sckp = sckp; a.sckh = sckh;
+  a.vc = static_cast<uint8_t*>(v_cache);
+  a.scvp = scvp; a.scvh = scvh;
+  a.num_slots = num_slots;
+  a.T = T;
+  a.Hq = static_cast<int>(Hq);
+  a.Hk = static_cast<int>(Hk);
+  a.D = static_cast<int>(D);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto al = [](const void* p, unsigned m) { return (reinterpret_cast<uintptr_t>(p) & (m - 1)) == 0; };
+  const bool fast = D == 128 && Hq % 4 == 0 && Hk % 4 == 0 && al(q, 16) && al(k, 16) && al(v, 16) &&
+                    sqt % 8 == 0 && sqh % 8 == 0 && skt % 8 == 0 && skh % 8 == 0 && svt % 8 == 0 &&
+                    svh % 8 == 0 && al(cos_sin_cache, 16) && al(k_cache, 16) && al(v_cache, 16) &&
+                    sckp % 8 == 0 && sckh % 8 == 0 && scvp % 8 == 0 && scvh % 8 == 0;
+  if (fast) {
+    const int64_t items = T * (Hq / 4 + 2 * (Hk / 4));
+    hipLaunchKernelGGL((qk_rope_kv_d128<kRopeBf16, 4>), dim3(static_cast<unsigned>((items + 3) / 4)),
+                       dim3(256), 0, st, a);
+  } else {
+    const int64_t items = T * (Hq + 2 * Hk);
+    hipLaunchKernelGGL(qk_rope_kv_generic<kRopeBf16>, dim3(static_cast<unsigned>((items + 3) / 4)),
+                       dim3(256), 0, st, a);
+  }
   return hipGetLastError() == hipSuccess ? FR_OK : FR_ELAUNCH;
 }
 

@@ -98,10 +98,15 @@ __device__ __forceinline__ float silu_in_range(float g) {
 // lane-strided elements, re-reading the row from global memory per pass.
 // A loop, not unrolled, so the vector kernel can also fall back to it for a
 // rare row without paying for it in registers.
+//
+// The RMS and SiLU modes round their intermediates to the activation dtype
+// (bf16 or fp16: torch's CPU ops compute in fp32 and store in that dtype);
+// the residual and the norm weight are in that dtype too.
 template <int MODE, int DT, bool QOUT>
 __device__ __forceinline__ void generic_row(const RowArgs& a, int64_t row, int lane) {
   using E = Elem<DT>;
   using T = typename E::T;
+  using H = Elem<DT == FR_DTYPE_FP32 ? FR_DTYPE_BF16 : DT>;  // 16-bit dtype of the RMS/SiLU modes
   const int64_t K = a.K;
   const T* xr = reinterpret_cast<const T*>(a.x) + row * a.ldx;
   uint16_t* rr = (MODE == kAddRms) ? a.res + row * a.ldr : nullptr;
@@ -112,8 +117,8 @@ __device__ __forceinline__ void generic_row(const RowArgs& a, int64_t row, int l
   if (MODE == kRms || MODE == kAddRms) for (int64_t e = lane; e < K; e += 64) {
     float val = E::load(xr + e);
     if (MODE == kAddRms) {
-      val = round_bf16(bf16_to_f32(rr[e]) + val);
-      rr[e] = static_cast<uint16_t>(pack_bf16x2(val, 0.0f) & 0xFFFFu);
+      val = H::round(H::load(rr + e) + val);
+      rr[e] = H::bits(val);
     }
     ss += val * val;
   }
@@ -125,19 +130,18 @@ __device__ __forceinline__ void generic_row(const RowArgs& a, int64_t row, int l
   auto value = [&](int64_t e) -> float {
     float val;
     if (MODE == kAddRms) {
-      val = bf16_to_f32(rr[e]);
+      val = H::load(rr + e);
     } else {
       val = E::load(xr + e);
     }
-    if (MODE == kSilu) val = round_bf16(silu_bf16(val) * E::load(xr + K + e));
-    if (MODE == kRms || MODE == kAddRms) val = round_bf16((val * rstd) * bf16_to_f32(a.w[e]));
+    if (MODE == kSilu) val = H::round(H::round(val / (1.0f + expf(-val))) * E::load(xr + K + e));
+    if (MODE == kRms || MODE == kAddRms) val = H::round((val * rstd) * H::load(a.w + e));
     return val;
   };
 
   if (!QOUT) {
     uint16_t* orow = reinterpret_cast<uint16_t*>(a.q) + row * a.ldq;
-    for (int64_t e = lane; e < K; e += 64)
-      orow[e] = static_cast<uint16_t>(pack_bf16x2(value(e), 0.0f) & 0xFFFFu);
+    for (int64_t e = lane; e < K; e += 64) orow[e] = H::bits(value(e));
     return;
   }
   float amax = 0.0f;
@@ -456,7 +460,6 @@ static int launch_rows(RowArgs a, int dtype, hipStream_t st) {
         hipLaunchKernelGGL((row_kernel_generic<MODE, FR_DTYPE_BF16, QOUT>), grid, dim3(256), 0, st, a);
         break;
       case FR_DTYPE_FP16:
-        if (MODE != kQuant) return FR_EUNSUPPORTED;
         hipLaunchKernelGGL((row_kernel_generic<MODE, FR_DTYPE_FP16, QOUT>), grid, dim3(256), 0, st, a);
         break;
       case FR_DTYPE_FP32:
@@ -496,8 +499,9 @@ int fr_quantize_weight_fp8(const void* w, int w_dtype, int64_t N, int64_t K, int
   return fr_per_token_quant_fp8(w, w_dtype, N, K, ldw, q, s, stream);
 }
 
-int fr_rms_quant_fp8(const void* x, int64_t ldx, void* residual, int64_t ldr, const void* w,
-                     int64_t M, int64_t H, float eps, void* q, float* s, void* stream) {
+int fr_rms_quant_fp8(const void* x, int x_dtype, int64_t ldx, void* residual, int64_t ldr,
+                     const void* w, int64_t M, int64_t H, float eps, void* q, float* s, void* stream) {
+  if (x_dtype != FR_DTYPE_BF16 && x_dtype != FR_DTYPE_FP16) return FR_EUNSUPPORTED;
   if ((M > 0 && H > 0) && (!x || !w || !q || !s)) return FR_EINVAL;
   RowArgs a{};
   a.x = static_cast<const uint16_t*>(x);
@@ -512,12 +516,12 @@ int fr_rms_quant_fp8(const void* x, int64_t ldx, void* residual, int64_t ldr, co
   a.K = H;
   a.eps = eps;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  return residual ? launch_rows<kAddRms, true>(a, FR_DTYPE_BF16, st)
-                  : launch_rows<kRms, true>(a, FR_DTYPE_BF16, st);
+  return residual ? launch_rows<kAddRms, true>(a, x_dtype, st) : launch_rows<kRms, true>(a, x_dtype, st);
 }
 
-int fr_rmsnorm(const void* x, int64_t ldx, void* residual, int64_t ldr, const void* w,
+int fr_rmsnorm(const void* x, int x_dtype, int64_t ldx, void* residual, int64_t ldr, const void* w,
                void* out, int64_t ldo, int64_t M, int64_t H, float eps, void* stream) {
+  if (x_dtype != FR_DTYPE_BF16 && x_dtype != FR_DTYPE_FP16) return FR_EUNSUPPORTED;
   if ((M > 0 && H > 0) && (!x || !w || !out)) return FR_EINVAL;
   RowArgs a{};
   a.x = static_cast<const uint16_t*>(x);
@@ -531,12 +535,12 @@ int fr_rmsnorm(const void* x, int64_t ldx, void* residual, int64_t ldr, const vo
   a.K = H;
   a.eps = eps;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  return residual ? launch_rows<kAddRms, false>(a, FR_DTYPE_BF16, st)
-                  : launch_rows<kRms, false>(a, FR_DTYPE_BF16, st);
+  return residual ? launch_rows<kAddRms, false>(a, x_dtype, st) : launch_rows<kRms, false>(a, x_dtype, st);
 }
 
-int fr_silu_quant_fp8(const void* x, int64_t ldx, int64_t M, int64_t d, void* q, float* s,
+int fr_silu_quant_fp8(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t d, void* q, float* s,
                       void* stream) {
+  if (x_dtype != FR_DTYPE_BF16 && x_dtype != FR_DTYPE_FP16) return FR_EUNSUPPORTED;
   if ((M > 0 && d > 0) && (!x || !q || !s)) return FR_EINVAL;
   RowArgs a{};
   a.x = static_cast<const uint16_t*>(x);
@@ -546,11 +550,12 @@ int fr_silu_quant_fp8(const void* x, int64_t ldx, int64_t M, int64_t d, void* q,
   a.s = s;
   a.M = M;
   a.K = d;
-  return launch_rows<kSilu, true>(a, FR_DTYPE_BF16, static_cast<hipStream_t>(stream));
+  return launch_rows<kSilu, true>(a, x_dtype, static_cast<hipStream_t>(stream));
 }
 
-int fr_silu_and_mul(const void* x, int64_t ldx, void* out, int64_t ldo, int64_t M, int64_t d,
+int fr_silu_and_mul(const void* x, int x_dtype, int64_t ldx, void* out, int64_t ldo, int64_t M, int64_t d,
                     void* stream) {
+  if (x_dtype != FR_DTYPE_BF16 && x_dtype != FR_DTYPE_FP16) return FR_EUNSUPPORTED;
   if ((M > 0 && d > 0) && (!x || !out)) return FR_EINVAL;
   RowArgs a{};
   a.x = static_cast<const uint16_t*>(x);
@@ -559,7 +564,7 @@ int fr_silu_and_mul(const void* x, int64_t ldx, void* out, int64_t ldo, int64_t 
   a.ldq = ldo;
   a.M = M;
   a.K = d;
-  return launch_rows<kSilu, false>(a, FR_DTYPE_BF16, static_cast<hipStream_t>(stream));
+  return launch_rows<kSilu, false>(a, x_dtype, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

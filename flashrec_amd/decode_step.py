@@ -204,6 +204,10 @@ class Qwen3FP8DecodeStep:
         self.hidden_in = (torch.randn(rows, shape.hidden, generator=gen, device=dev)).to(torch.bfloat16)
         self._graph: Optional[torch.cuda.CUDAGraph] = None
         self._out = None
+        # probe(layer_id, stage, *tensors): called at each stage boundary of a
+        # layer when set (tests compare every stage with the oracle); it must
+        # copy what it keeps, later stages update some tensors in place
+        self.probe = None
         self.trie = None
         if trie_items > 0:
             self._init_beam(requests, beams, trie_items, trie_levels, trie_codes, gen, step)
@@ -214,6 +218,7 @@ class Qwen3FP8DecodeStep:
         s = self.shape
         t = int(q_fp8.shape[0])
         qkv = L.qkv_proj.forward_fp8(q_fp8, a_scale, (t, s.hidden), torch.bfloat16)
+        self._tap(L, "qkv", qkv)
         heads = qkv.view(t, s.q_heads + 2 * s.kv_heads, s.head_dim)
         q = heads[:, : s.q_heads]
         k = heads[:, s.q_heads: s.q_heads + s.kv_heads]
@@ -223,9 +228,17 @@ class Qwen3FP8DecodeStep:
             L.q_norm.eps, self.rotary.cos_sin_cache, self.pool.k[L.layer_id], self.pool.v[L.layer_id])
         if not stored:
             raise RuntimeError("fused QK-norm/RoPE/KV write rejected its inputs")
+        self._tap(L, "rope", q)
         # q stays a strided view of qkv: the attention kernel takes row and head strides
         o = self.attn.forward(q, k, v, L.layer_id, self.batch, skip_store=True)
-        return L.o_proj(o.reshape(t, -1))
+        self._tap(L, "attn", o)
+        out = L.o_proj(o.reshape(t, -1))
+        self._tap(L, "o", out)
+        return out
+
+    def _tap(self, L: _Layer, stage: str, *tensors) -> None:
+        if self.probe is not None:
+            self.probe(L.layer_id, stage, *tensors)
 
     def _layer(self, L: _Layer, x: torch.Tensor, residual: Optional[torch.Tensor]):
         """qwen3.py:197-210 (fused RMSNorm->fp8 path) and the MLP of :146-171."""
@@ -234,12 +247,17 @@ class Qwen3FP8DecodeStep:
             q_fp8, a_scale = L.input_layernorm.quant_fp8(x)
         else:
             q_fp8, a_scale, residual = L.input_layernorm.quant_fp8(x, residual)
+        self._tap(L, "ln_in", q_fp8, a_scale, residual)
         hidden = self._attention(L, q_fp8, a_scale)
         q_fp8, a_scale, residual = L.post_attention_layernorm.quant_fp8(hidden, residual)
+        self._tap(L, "ln_post", q_fp8, a_scale, residual)
         t = int(q_fp8.shape[0])
         gu = L.gate_up_proj.forward_fp8(q_fp8, a_scale, (t, self.shape.hidden), torch.bfloat16)
+        self._tap(L, "gate_up", gu)
         y_fp8, y_scale = silu_and_mul_per_token_quant_fp8(gu)
+        self._tap(L, "silu", y_fp8, y_scale)
         hidden = L.down_proj.forward_fp8(y_fp8, y_scale, (t, self.shape.intermediate), torch.bfloat16)
+        self._tap(L, "down", hidden)
         return hidden, residual
 
     def forward(self, x: Optional[torch.Tensor] = None, layers: Optional[int] = None) -> torch.Tensor:

@@ -2,7 +2,7 @@
 
 Reference: python/flashrec/kernel/rms_fp8.py:74-145.  The reference's CUDA
 path is a Triton kernel that quantizes the fp32 normalised value; its CPU
-path rounds the normalised row to bf16 first (``rmsnorm`` then
+path rounds the normalised row to the activation dtype (bf16 or fp16) first (``rmsnorm`` then
 ``per_token_quant_fp8``, rms_fp8.py:128-130 / :141-145).  This kernel
 reproduces the latter bit for bit, in one pass over HBM.
 """
@@ -13,7 +13,7 @@ from typing import Optional
 
 import torch
 
-from flashrec_amd._lib import call, require_device, stream_of
+from flashrec_amd._lib import DTYPE_CODE, call, require_device, stream_of
 
 _FP8_MAX = 448.0
 
@@ -25,12 +25,14 @@ def _launch(
     residual: Optional[torch.Tensor],
 ) -> tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
     require_device(x, residual)
-    if x.dtype != torch.bfloat16 or (residual is not None and residual.dtype != torch.bfloat16):
-        raise TypeError("rms_fp8 takes bf16 activations")
+    if x.dtype not in (torch.bfloat16, torch.float16) or (residual is not None and residual.dtype != x.dtype):
+        raise TypeError("rms_fp8 takes bf16 or fp16 activations (and a residual of the same dtype)")
     orig = x.shape
     hidden = int(weight.numel())
     x2 = x.reshape(-1, hidden).contiguous()
-    w = weight.reshape(-1).to(device=x.device, dtype=torch.bfloat16).contiguous()
+    # the norm weight in the activations' dtype, as the reference's fused
+    # path passes it (rms_fp8.py:86)
+    w = weight.reshape(-1).to(device=x.device, dtype=x.dtype).contiguous()
     rows = int(x2.shape[0])
     r2 = None
     if residual is not None:
@@ -39,7 +41,7 @@ def _launch(
             raise ValueError(f"residual {tuple(residual.shape)} does not match x {tuple(orig)}")
     y = torch.empty(x2.shape, dtype=torch.float8_e4m3fn, device=x2.device)
     scale = torch.empty((rows, 1), dtype=torch.float32, device=x2.device)
-    call("fr_rms_quant_fp8", x2.data_ptr(), x2.stride(0),
+    call("fr_rms_quant_fp8", x2.data_ptr(), DTYPE_CODE[x.dtype], x2.stride(0),
          None if r2 is None else r2.data_ptr(), 0 if r2 is None else r2.stride(0),
          w.data_ptr(), rows, hidden, float(eps), y.data_ptr(), scale.data_ptr(), stream_of(x))
     res_out = r2.reshape(residual.shape) if r2 is not None else None

@@ -18,8 +18,12 @@ from flashrec_amd._lib import DTYPE_CODE, call, ptr, require_device, stream_of
 _FP8_MAX = 448.0
 
 
-def _bf16_vec(weight: torch.Tensor, device: torch.device) -> torch.Tensor:
-    return weight.reshape(-1).to(device=device, dtype=torch.bfloat16).contiguous()
+_HALF = (torch.bfloat16, torch.float16)
+
+
+def _vec(weight: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """The norm weight as a contiguous vector in the activations' dtype."""
+    return weight.reshape(-1).to(device=x.device, dtype=x.dtype).contiguous()
 
 
 def _rows(x: torch.Tensor, width: int) -> torch.Tensor:
@@ -34,14 +38,14 @@ def _rows(x: torch.Tensor, width: int) -> torch.Tensor:
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     """``(x * rsqrt(mean(x^2) + eps)) * weight`` per row (sglops.py:33-45)."""
     require_device(x)
-    if x.dtype != torch.bfloat16:
-        raise TypeError(f"rmsnorm takes bf16 activations, got {x.dtype}")
+    if x.dtype not in _HALF:
+        raise TypeError(f"rmsnorm takes bf16/fp16 activations, got {x.dtype}")
     orig = x.shape
     hidden = int(weight.numel())
     x2 = _rows(x, hidden)
-    w = _bf16_vec(weight, x.device)
+    w = _vec(weight, x)
     out = torch.empty(x2.shape, dtype=x.dtype, device=x.device)
-    call("fr_rmsnorm", x2.data_ptr(), x2.stride(0), None, 0, w.data_ptr(), out.data_ptr(),
+    call("fr_rmsnorm", x2.data_ptr(), DTYPE_CODE[x.dtype], x2.stride(0), None, 0, w.data_ptr(), out.data_ptr(),
          out.stride(0), x2.shape[0], hidden, float(eps), stream_of(x))
     return out.view(orig)
 
@@ -52,13 +56,13 @@ def fused_add_rmsnorm(
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """``residual += x`` then RMSNorm(residual). Mutates both (sglops.py:48-61)."""
     require_device(x, residual)
-    if x.dtype != torch.bfloat16 or residual.dtype != torch.bfloat16:
-        raise TypeError("fused_add_rmsnorm takes bf16 x and residual")
+    if x.dtype not in _HALF or residual.dtype != x.dtype:
+        raise TypeError("fused_add_rmsnorm takes bf16 or fp16 x and a residual of the same dtype")
     hidden = int(weight.numel())
     x2 = x.reshape(-1, hidden).contiguous()
     r2 = residual.reshape(-1, hidden).contiguous()
-    w = _bf16_vec(weight, x.device)
-    call("fr_rmsnorm", x2.data_ptr(), x2.stride(0), r2.data_ptr(), r2.stride(0), w.data_ptr(),
+    w = _vec(weight, x)
+    call("fr_rmsnorm", x2.data_ptr(), DTYPE_CODE[x.dtype], x2.stride(0), r2.data_ptr(), r2.stride(0), w.data_ptr(),
          x2.data_ptr(), x2.stride(0), x2.shape[0], hidden, float(eps), stream_of(x))
     return x2.reshape(x.shape), r2.reshape(residual.shape)
 
@@ -119,7 +123,6 @@ def fp8_scaled_mm(
     bias: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """a: [M,K] fp8, b: [K,N] fp8 (column-major), scale_a: [M,1], scale_b: [N] (sglops.py:99-140)."""
-    require_device(a_fp8, b_fp8)
     if a_fp8.dtype != torch.float8_e4m3fn or b_fp8.dtype != torch.float8_e4m3fn:
         raise TypeError("fp8_scaled_mm takes float8_e4m3fn operands")
     if out_dtype not in (torch.bfloat16, torch.float16, torch.float32):
@@ -128,6 +131,9 @@ def fp8_scaled_mm(
         raise ValueError(f"shape mismatch: a {tuple(a_fp8.shape)} b {tuple(b_fp8.shape)}")
     m, k = int(a_fp8.shape[0]), int(a_fp8.shape[1])
     n = int(b_fp8.shape[1])
+    if bias is not None and bias.numel() != n:
+        raise ValueError(f"bias has {bias.numel()} values, the output has {n} columns")
+    require_device(a_fp8, b_fp8)
     a = a_fp8 if a_fp8.stride(1) == 1 and (m <= 1 or a_fp8.stride(0) >= k) else a_fp8.contiguous()
     b = b_fp8
     if not (b.stride(0) == 1 and (n <= 1 or b.stride(1) >= k)):
@@ -143,7 +149,7 @@ def fp8_scaled_mm(
     lda = a.stride(0) if m > 1 else k
     ldb = b.stride(1) if n > 1 else k
     call("fr_fp8_scaled_mm", a.data_ptr(), lda, b.data_ptr(), ldb, sa.data_ptr(), sa.numel(),
-         sb.data_ptr(), sb.numel(), ptr(bias_t), out.data_ptr(), out.stride(0), m, n, k,
+         sb.data_ptr(), sb.numel(), ptr(bias_t), 0 if bias_t is None else n, out.data_ptr(), out.stride(0), m, n, k,
          DTYPE_CODE[out_dtype], stream_of(a))
     return out
 
@@ -152,15 +158,15 @@ def fp8_scaled_mm(
 def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
     """SwiGLU: ``silu(x[..., :d]) * x[..., d:]`` with ``d = last_dim // 2`` (sglops.py:143-151)."""
     require_device(x)
-    if x.dtype != torch.bfloat16:
-        raise TypeError(f"silu_and_mul takes bf16, got {x.dtype}")
+    if x.dtype not in _HALF:
+        raise TypeError(f"silu_and_mul takes bf16/fp16, got {x.dtype}")
     last = int(x.shape[-1])
     if last % 2:
         raise ValueError("silu_and_mul needs an even last dimension")
     d = last // 2
     x2 = _rows(x, last)
     out = torch.empty((x2.shape[0], d), dtype=x.dtype, device=x.device)
-    call("fr_silu_and_mul", x2.data_ptr(), x2.stride(0), out.data_ptr(), out.stride(0),
+    call("fr_silu_and_mul", x2.data_ptr(), DTYPE_CODE[x.dtype], x2.stride(0), out.data_ptr(), out.stride(0),
          x2.shape[0], d, stream_of(x))
     return out.view(*x.shape[:-1], d)
 
@@ -177,17 +183,47 @@ def apply_rope_and_store_kv(
     head_size: int,
     cos_sin_cache: torch.Tensor,
 ) -> bool:
-    """Fused RoPE + KV store for matching dtypes (sglops.py:154-204).
+    """RoPE of ``query`` / ``key`` in place, then ``k_cache[loc] = key``,
+    ``v_cache[loc] = value``, in one kernel (sglops.py:154-204).
 
-    The reference returns False whenever the cache dtype differs from the
-    activations (every fp8-KV configuration), and the FP8 path always has an
-    fp8 cache, so this returns False for that case and the caller goes
-    through ``fused_qk_norm_rope_store_fp8`` / ``TokenToKVPool.store``.
+    As in the reference this is the matching-dtype path: it returns False
+    when a cache's dtype differs from the activations' (an fp8 pool goes
+    through ``fused_qk_norm_rope_store_fp8`` or ``TokenToKVPool.store``), and
+    for layouts the kernel does not take (head dim > 128 or odd, non-unit
+    inner strides, a cache whose rows are not ``[H_kv, head_size]``).
     """
-    require_device(query, key, value)
+    require_device(query, key, value, k_cache, v_cache)
     if key.dtype != k_cache.dtype or value.dtype != v_cache.dtype:
         return False
-    return False
+    if not (query.dtype == key.dtype == value.dtype == torch.bfloat16):
+        return False
+    d = int(head_size)
+    t = int(positions.numel())
+    if d <= 0 or d > 128 or d % 2 or int(cos_sin_cache.shape[-1]) != d:
+        return False
+    q3 = query.view(t, -1, d)
+    k3 = key.view(t, -1, d)
+    v3 = value.view(t, -1, d)
+    hk = int(k3.shape[1])
+    if int(v3.shape[1]) != hk or q3.stride(-1) != 1 or k3.stride(-1) != 1 or v3.stride(-1) != 1:
+        return False
+    slots = int(k_cache.shape[0])
+    if k_cache.numel() != slots * hk * d or v_cache.shape != k_cache.shape:
+        return False
+    kc = k_cache.view(slots, hk, d)
+    vc = v_cache.view(slots, hk, d)
+    if kc.stride(-1) != 1 or vc.stride(-1) != 1:
+        return False
+    pos = positions.reshape(-1).to(dtype=torch.int64).contiguous()
+    loc64 = loc.reshape(-1).to(dtype=torch.int64).contiguous()
+    if int(loc64.numel()) != t:
+        raise ValueError(f"loc has {loc64.numel()} slots for {t} tokens")
+    cs = cos_sin_cache.to(device=query.device, dtype=torch.float32).contiguous()
+    call("fr_rope_store_kv_bf16", q3.data_ptr(), q3.stride(0), q3.stride(1), k3.data_ptr(),
+         k3.stride(0), k3.stride(1), v3.data_ptr(), v3.stride(0), v3.stride(1), pos.data_ptr(),
+         loc64.data_ptr(), cs.data_ptr(), cs.shape[0], kc.data_ptr(), kc.stride(0), kc.stride(1),
+         vc.data_ptr(), vc.stride(0), vc.stride(1), slots, t, q3.shape[1], hk, d, stream_of(query))
+    return True
 
 
 @torch.compiler.disable
@@ -200,13 +236,13 @@ def store_kv_cache(
 ) -> None:
     """``k_cache[loc] = k; v_cache[loc] = v`` on rows of width row_dim (sglops.py:207-222).
 
-    Caches are e4m3 ``[slots, row_dim]``; k/v are e4m3 (copied) or bf16
-    (converted with torch's ``.to(float8_e4m3fn)`` rounding).  Slots outside
-    ``[0, slots)`` are skipped instead of raising an IndexError.
+    e4m3 caches take e4m3 k/v (copied) or bf16 k/v (converted with torch's
+    ``.to(float8_e4m3fn)`` rounding); bf16 caches take bf16 k/v.  Slots
+    outside ``[0, slots)`` are skipped instead of raising an IndexError.
     """
     require_device(k_cache, v_cache, k, v)
-    if k_cache.dtype != torch.float8_e4m3fn or v_cache.dtype != torch.float8_e4m3fn:
-        raise TypeError("store_kv_cache writes float8_e4m3fn caches")
+    if k_cache.dtype != v_cache.dtype or k_cache.dtype not in (torch.float8_e4m3fn, torch.bfloat16):
+        raise TypeError("store_kv_cache writes float8_e4m3fn or bfloat16 caches")
     slots = int(k_cache.shape[0])
     row_dim = int(k_cache[0].numel()) if slots else int(k.shape[-1])
     kc = k_cache.view(slots, row_dim)
@@ -215,12 +251,19 @@ def store_kv_cache(
     n = int(loc64.numel())
     k2 = k.reshape(n, row_dim)
     v2 = v.reshape(n, row_dim)
-    if k2.dtype != v2.dtype or k2.dtype not in (torch.bfloat16, torch.float8_e4m3fn):
-        raise TypeError("k/v must both be bf16 or both float8_e4m3fn")
     if k2.stride(-1) != 1:
         k2 = k2.contiguous()
     if v2.stride(-1) != 1:
         v2 = v2.contiguous()
+    if k_cache.dtype == torch.bfloat16:
+        if k2.dtype != torch.bfloat16 or v2.dtype != torch.bfloat16:
+            raise TypeError("a bf16 cache takes bf16 k/v")
+        call("fr_store_kv_bf16", k2.data_ptr(), k2.stride(0), v2.data_ptr(), v2.stride(0),
+             loc64.data_ptr(), kc.data_ptr(), kc.stride(0), vc.data_ptr(), vc.stride(0), slots, n,
+             row_dim, stream_of(k_cache))
+        return
+    if k2.dtype != v2.dtype or k2.dtype not in (torch.bfloat16, torch.float8_e4m3fn):
+        raise TypeError("k/v must both be bf16 or both float8_e4m3fn")
     call("fr_store_kv_fp8", k2.data_ptr(), k2.stride(0), v2.data_ptr(), v2.stride(0),
          DTYPE_CODE[k2.dtype], loc64.data_ptr(), kc.data_ptr(), kc.stride(0), vc.data_ptr(),
          vc.stride(0), slots, n, row_dim, stream_of(k_cache))
@@ -228,10 +271,17 @@ def store_kv_cache(
 
 @torch.compiler.disable
 def log_softmax_f32(logits: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Row-wise ``log_softmax`` of fp32 logits (the tail of logits.py:118-120)."""
-    require_device(logits)
+    """Row-wise ``log_softmax`` of fp32 logits (the tail of logits.py:118-120).
+
+    ``out`` (default: a new tensor) may be ``logits`` itself; it must be fp32
+    of the logits' shape and device with unit inner stride."""
     if logits.dtype != torch.float32 or logits.dim() != 2 or logits.stride(1) != 1:
         raise TypeError("log_softmax_f32 takes 2-D fp32 logits with unit inner stride")
+    if out is not None and (out.dtype != torch.float32 or tuple(out.shape) != tuple(logits.shape)
+                            or out.stride(1) != 1 or out.device != logits.device):
+        raise ValueError("log_softmax_f32: out must be fp32 on the logits' device, of the logits' "
+                         f"shape {tuple(logits.shape)}, with unit inner stride")
+    require_device(logits)
     if out is None:
         out = torch.empty_like(logits)
     call("fr_log_softmax_f32", logits.data_ptr(), logits.stride(0), out.data_ptr(),

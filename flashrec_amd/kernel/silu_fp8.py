@@ -10,7 +10,7 @@ from __future__ import annotations
 
 import torch
 
-from flashrec_amd._lib import call, require_device, stream_of
+from flashrec_amd._lib import DTYPE_CODE, call, require_device, stream_of
 
 _FP8_MAX = 448.0
 
@@ -21,8 +21,8 @@ def silu_and_mul_per_token_quant_fp8(
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """``silu(x[..., :d]) * x[..., d:]`` then per-token e4m3. ``d = last_dim // 2``."""
     require_device(x)
-    if x.dtype != torch.bfloat16:
-        raise TypeError(f"silu_and_mul_per_token_quant_fp8 takes bf16, got {x.dtype}")
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"silu_and_mul_per_token_quant_fp8 takes bf16 or fp16, got {x.dtype}")
     last = int(x.shape[-1])
     if last % 2 != 0:
         raise ValueError("silu_and_mul_per_token_quant_fp8 needs an even last dimension")
@@ -31,6 +31,6 @@ def silu_and_mul_per_token_quant_fp8(
     rows = int(x2.shape[0])
     y = torch.empty((rows, d), dtype=torch.float8_e4m3fn, device=x2.device)
     scale = torch.empty((rows, 1), dtype=torch.float32, device=x2.device)
-    call("fr_silu_quant_fp8", x2.data_ptr(), x2.stride(0), rows, d, y.data_ptr(),
+    call("fr_silu_quant_fp8", x2.data_ptr(), DTYPE_CODE[x.dtype], x2.stride(0), rows, d, y.data_ptr(),
          scale.data_ptr(), stream_of(x))
     return y, scale

@@ -1,12 +1,28 @@
-"""Linear with W8A8 per-channel fp8, mirroring ``flashrec.layers.linear``.
+"""W8A8 linear layer: a drop-in for ``flashrec.layers.linear`` on the fp8 path.
 
-Reference: python/flashrec/layers/linear.py.  Same public names and weight
-layout: the fp8 weight is kept as a ``[K, N]`` column-major view of the
-``[N, K]`` e4m3 matrix (``_fp8_weight``) with a ``[N]`` fp32 scale
-(``_fp8_scale``).  Quantisation, activation quant and the GEMM run in HIP.
-Difference from the reference: ``forward`` does not catch fp8 GEMM errors
-and silently dequantise to a bf16 ``F.linear`` (linear.py:124-131); a failing
-kernel raises.
+Interface kept from python/flashrec/layers/linear.py (what FlashRec's model
+code and tests read):
+
+* ``quantize_weight_fp8(w) -> (codes [N, K] e4m3, scale [N] fp32)`` (:26-32);
+* ``as_channel_scale(scale, out_features, device=None)`` (:35-57): one value
+  is broadcast to every output channel, ``out_features`` values are taken as
+  they are, anything else (block-wise scales) is a ``ValueError``;
+* ``Linear(in_features, out_features, bias=False)`` with ``load(weight, bias,
+  quantize_fp8, weight_scale)``, ``forward(x)`` and ``forward_fp8(q, a_scale,
+  orig_shape, out_dtype)`` (:66-151), and the attributes ``_use_fp8``,
+  ``_fp8_weight`` (the ``[K, N]`` column-major view of the ``[N, K]`` codes)
+  and ``_fp8_scale`` (``[N]`` fp32).
+
+Layout here: the codes and their scales are registered buffers
+(``w_codes`` ``[N, K]`` row-major, ``w_scale`` ``[N]``), so ``module.to()``
+moves them with the module (a float cast of the module leaves them as they
+are); ``_fp8_weight`` / ``_fp8_scale`` are views of them.  A call runs on the
+HIP library only: per-token e4m3 quantisation of the activations, then the
+W8A8 GEMM with both scales and the optional bias applied in its epilogue.
+
+Behaviour that differs from the reference on purpose: a failing fp8 GEMM
+raises instead of being retried as a dequantised bf16 ``F.linear``
+(:124-131); a bias whose length is not ``out_features`` is refused at load.
 """
 
 from __future__ import annotations
@@ -20,139 +36,148 @@ import torch.nn.functional as F
 from flashrec_amd._lib import DTYPE_CODE, call, require_device, stream_of
 from flashrec_amd.kernel.sglops import fp8_scaled_mm, per_token_quant_fp8
 
-_FP8_MAX = 448.0
-
-
-def _is_fp8(dtype: torch.dtype) -> bool:
-    return dtype in (
-        torch.float8_e4m3fn,
-        getattr(torch, "float8_e5m2", torch.float8_e4m3fn),
-    )
+_E4M3 = torch.float8_e4m3fn
+_FP8_DTYPES = frozenset({torch.float8_e4m3fn, torch.float8_e5m2})
+_HALF_DTYPES = (torch.bfloat16, torch.float16)
 
 
 def quantize_weight_fp8(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """Per-channel absmax quantize to e4m3. Returns (fp8 [N,K], scale [N]) (linear.py:26-32)."""
+    """Per-output-channel absmax e4m3 codes of a ``[N, K]`` weight and their
+    fp32 scales (amax / 448), in one HIP kernel (linear.py:26-32)."""
     require_device(weight)
+    if weight.dim() != 2:
+        raise ValueError(f"quantize_weight_fp8 takes a [N, K] matrix, got shape {tuple(weight.shape)}")
     if weight.dtype not in (torch.bfloat16, torch.float16, torch.float32):
         raise TypeError(f"quantize_weight_fp8 takes bf16/fp16/fp32, got {weight.dtype}")
-    w = weight if weight.stride(-1) == 1 else weight.contiguous()
-    n, k = int(w.shape[0]), int(w.shape[1])
-    q = torch.empty((n, k), dtype=torch.float8_e4m3fn, device=w.device)
-    s = torch.empty((n,), dtype=torch.float32, device=w.device)
-    call("fr_quantize_weight_fp8", w.data_ptr(), DTYPE_CODE[w.dtype], n, k,
-         w.stride(0) if n > 1 else k, q.data_ptr(), s.data_ptr(), stream_of(w))
-    return q, s
+    src = weight.contiguous() if weight.stride(-1) != 1 else weight
+    rows, cols = src.shape
+    codes = torch.empty((rows, cols), dtype=_E4M3, device=src.device)
+    scale = torch.empty((rows,), dtype=torch.float32, device=src.device)
+    row_stride = src.stride(0) if rows > 1 else cols
+    call("fr_quantize_weight_fp8", src.data_ptr(), DTYPE_CODE[src.dtype], rows, cols, row_stride,
+         codes.data_ptr(), scale.data_ptr(), stream_of(src))
+    return codes, scale
 
 
-def as_channel_scale(
-    scale: torch.Tensor,
-    out_features: int,
-    device: torch.device | None = None,
-) -> torch.Tensor:
-    """Per-tensor scale -> length ``out_features``; per-channel unchanged (linear.py:35-57)."""
-    s = scale.detach().to(dtype=torch.float32).reshape(-1)
-    if device is not None:
-        s = s.to(device=device)
-    n = int(s.numel())
-    if n == 1:
-        return s.expand(out_features).contiguous()
-    if n == out_features:
-        return s.contiguous()
+def as_channel_scale(scale: torch.Tensor, out_features: int,
+                     device: Optional[torch.device] = None) -> torch.Tensor:
+    """A checkpoint's ``weight_scale`` as ``[out_features]`` fp32 (linear.py:35-57).
+
+    Fused projections concatenate per-matrix scalars, so callers expand each
+    source matrix's scale before concatenating (see ``flashrec_amd.weight``).
+    """
+    flat = scale.detach().reshape(-1).to(device=device, dtype=torch.float32)
+    count = flat.numel()
+    if count == out_features:
+        return flat.contiguous()
+    if count == 1:
+        return flat.repeat(out_features)
     raise ValueError(
-        f"FP8 weight_scale has {n} values, expected 1 (per-tensor) or "
-        f"{out_features} (per-channel); block-wise scales are not supported"
-    )
-
-
-def _channel_scale(scale: torch.Tensor, out_features: int, device: torch.device) -> torch.Tensor:
-    return as_channel_scale(scale, out_features, device)
+        f"weight_scale holds {count} values for a layer of {out_features} output channels: "
+        "only a per-tensor (1) or per-channel scale is supported, not block-wise scales")
 
 
 class Linear(nn.Module):
+    """``y = x W^T (+ b)``, with ``W`` held as per-channel e4m3 codes when
+    loaded from an fp8 checkpoint or with ``quantize_fp8=True``, otherwise as
+    a plain ``weight`` parameter (the reference's unquantised layers)."""
+
     def __init__(self, in_features: int, out_features: int, bias: bool = False):
         super().__init__()
-        self.in_features = in_features
-        self.out_features = out_features
+        self.in_features = int(in_features)
+        self.out_features = int(out_features)
         self.weight = nn.Parameter(torch.empty(0), requires_grad=False)
-        self.bias = (
-            nn.Parameter(torch.empty(out_features), requires_grad=False) if bias else None
-        )
-        self._fp8_weight: Optional[torch.Tensor] = None  # [K, N] column-major
-        self._fp8_scale: Optional[torch.Tensor] = None  # [N]
-        self._use_fp8 = False
+        self.bias = nn.Parameter(torch.empty(self.out_features), requires_grad=False) if bias else None
+        self.register_buffer("w_codes", None)
+        self.register_buffer("w_scale", None)
 
-    def load(
-        self,
-        weight: torch.Tensor,
-        bias: torch.Tensor | None = None,
-        quantize_fp8: bool = False,
-        weight_scale: torch.Tensor | None = None,
-    ):
-        """Load bf16 / fp8 weights (linear.py:81-116)."""
-        device = weight.device
+    # --- the attributes FlashRec's callers read ---------------------------------
+    @property
+    def _use_fp8(self) -> bool:
+        return self.w_codes is not None
+
+    @property
+    def _fp8_weight(self) -> Optional[torch.Tensor]:
+        """``[K, N]`` column-major view of the ``[N, K]`` codes."""
+        return None if self.w_codes is None else self.w_codes.t()
+
+    @property
+    def _fp8_scale(self) -> Optional[torch.Tensor]:
+        return self.w_scale
+
+    def _apply(self, fn, recurse=True):
+        # Module.to() / .cuda() / .half() move the codes and scales to the new
+        # device but never cast them: a float cast would destroy the e4m3 codes
+        codes, scale = self.w_codes, self.w_scale
+        self.w_codes = self.w_scale = None
+        try:
+            super()._apply(fn, recurse)
+        finally:
+            if codes is not None:
+                dev = fn(torch.empty(0, device=codes.device)).device
+                self.w_codes = codes.to(device=dev)
+                self.w_scale = scale.to(device=dev)
+        return self
+
+    # --- loading ---------------------------------------------------------------
+    def load(self, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
+             quantize_fp8: bool = False, weight_scale: Optional[torch.Tensor] = None) -> None:
+        """Take a ``[N, K]`` weight: fp8 codes (+ optional per-tensor or
+        per-channel ``weight_scale``, default 1), or bf16/fp16/fp32 that is
+        quantised here when ``quantize_fp8`` is set and kept as is otherwise
+        (linear.py:81-116)."""
+        if weight.dim() == 2 and weight.shape[0] != self.out_features:
+            raise ValueError(f"weight has {weight.shape[0]} rows, layer has {self.out_features} outputs")
         if weight.dtype == torch.uint8 and weight_scale is not None:
-            raise NotImplementedError(
-                "NVFP4 Linear needs an official NVFP4 checkpoint "
-                "(packed uint8 + block scale); online FP8->NVFP4 is not supported"
-            )
-        if _is_fp8(weight.dtype):
+            # packed 4-bit weights with block scales: a format this path does
+            # not take (the reference refuses online conversion to it as well)
+            raise NotImplementedError("packed uint8 weights with block scales (NVFP4) are not supported "
+                                      "by the fp8 linear; load an fp8 or bf16 checkpoint")
+        if weight.dtype in _FP8_DTYPES:
             if weight_scale is None:
-                scale = torch.ones(self.out_features, dtype=torch.float32, device=device)
+                scale = torch.ones(self.out_features, dtype=torch.float32, device=weight.device)
             else:
-                scale = _channel_scale(weight_scale, self.out_features, device)
-            self._fp8_weight = weight.t()
-            self._fp8_scale = scale
-            self._use_fp8 = True
+                scale = as_channel_scale(weight_scale, self.out_features, weight.device)
+            self._set_codes(weight, scale)
         elif quantize_fp8:
-            q, scale = quantize_weight_fp8(weight)
-            self._fp8_weight = q.t()
-            self._fp8_scale = scale.to(device=device)
-            self._use_fp8 = True
+            self._set_codes(*quantize_weight_fp8(weight))
         else:
             self.weight = nn.Parameter(weight, requires_grad=False)
-            self._use_fp8 = False
+            self.w_codes = None
+            self.w_scale = None
         if bias is not None:
-            self.bias = nn.Parameter(bias, requires_grad=False)
+            if bias.numel() != self.out_features:
+                raise ValueError(f"bias has {bias.numel()} values, layer has {self.out_features} outputs")
+            self.bias = nn.Parameter(bias.reshape(self.out_features), requires_grad=False)
 
+    def _set_codes(self, codes: torch.Tensor, scale: torch.Tensor) -> None:
+        # ``codes`` is the [N, K] matrix (a transposed [K, N] view stays a view)
+        self.w_codes = codes
+        self.w_scale = scale.to(device=codes.device, dtype=torch.float32).reshape(self.out_features)
+        self.weight = nn.Parameter(torch.empty(0, device=codes.device), requires_grad=False)
+
+    # --- calls -----------------------------------------------------------------
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if self._use_fp8 and self._fp8_weight is not None and self._fp8_scale is not None:
-            return self._fp8_forward(x)
-        return F.linear(x, self.weight.to(dtype=x.dtype), self.bias)
+        if self.w_codes is None:
+            return F.linear(x, self.weight.to(dtype=x.dtype), self.bias)
+        rows = x.reshape(-1, x.shape[-1])
+        if not rows.is_contiguous():
+            rows = rows.contiguous()
+        codes, scale = per_token_quant_fp8(rows)
+        out_dtype = x.dtype if x.dtype in _HALF_DTYPES else torch.bfloat16
+        return self.forward_fp8(codes, scale, tuple(x.shape), out_dtype)
 
-    def forward_fp8(
-        self,
-        q: torch.Tensor,
-        a_scale: torch.Tensor,
-        orig_shape: tuple,
-        out_dtype: torch.dtype,
-    ) -> torch.Tensor:
-        """GEMM from a pre-quantized activation. ``q`` is [M, K] e4m3 (linear.py:134-142)."""
-        return self._fp8_mm(q, a_scale, orig_shape, out_dtype)
-
-    def _fp8_forward(self, x: torch.Tensor) -> torch.Tensor:
-        orig = x.shape
-        x2 = x.reshape(-1, orig[-1]).contiguous()
-        q, a_scale = per_token_quant_fp8(x2)
-        out_dtype = x.dtype if x.dtype in (torch.bfloat16, torch.float16) else torch.bfloat16
-        return self._fp8_mm(q, a_scale, orig, out_dtype)
-
-    def _fp8_mm(
-        self,
-        q: torch.Tensor,
-        a_scale: torch.Tensor,
-        orig_shape: tuple,
-        out_dtype: torch.dtype,
-    ) -> torch.Tensor:
-        b = self._fp8_weight
-        b_scale = self._fp8_scale
-        assert b is not None and b_scale is not None
-        device = q.device
-        if b.device != device:
-            b = b.to(device=device)
-            self._fp8_weight = b
-        if b_scale.device != device:
-            b_scale = b_scale.to(device=device)
-            self._fp8_scale = b_scale
-        bias = self.bias.to(dtype=out_dtype) if self.bias is not None else None
-        out = fp8_scaled_mm(q, b, a_scale, b_scale, out_dtype, bias)
-        return out.view(*orig_shape[:-1], self.out_features)
+    def forward_fp8(self, q: torch.Tensor, a_scale: torch.Tensor, orig_shape: tuple,
+                    out_dtype: torch.dtype) -> torch.Tensor:
+        """GEMM of already quantised ``[M, K]`` e4m3 rows with their ``[M, 1]``
+        scales; the result has shape ``orig_shape[:-1] + (out_features,)``
+        (linear.py:134-142, 153-172)."""
+        if self.w_codes is None:
+            raise RuntimeError("Linear.forward_fp8 needs fp8 weights (load an fp8 checkpoint "
+                               "or pass quantize_fp8=True)")
+        if self.w_codes.device != q.device:
+            raise ValueError(f"activations on {q.device}, fp8 weights on {self.w_codes.device}: "
+                             "move the module with .to() first")
+        bias = None if self.bias is None else self.bias.to(dtype=out_dtype)
+        out = fp8_scaled_mm(q, self.w_codes.t(), a_scale, self.w_scale, out_dtype, bias)
+        return out.view(*tuple(orig_shape)[:-1], self.out_features)

@@ -1,18 +1,34 @@
-"""SID-restricted lm_head mirroring ``flashrec.logits.RestrictedLMHead``.
+"""SID-restricted lm_head + log_softmax: a drop-in for ``flashrec.logits.RestrictedLMHead``
+(python/flashrec/logits.py:11-166).
 
-Reference: python/flashrec/logits.py:11-166.  Same API (``bind``,
-``bind_codebook``, ``compute``, ``compute_level``, ``compute_into``).  With
-``fp8=True`` (the north-star upgrade; the reference always runs a bf16
-``F.linear``), ``bind`` quantises the restricted weight slice per output
-channel once, and every call runs per-token e4m3 quant of the hidden rows,
-the W8A8 GEMM with fp32 logits, and an in-place fp32 log_softmax -- three HIP
-kernels, no host sync, graph-capturable.  With ``fp8=False`` it behaves like
-the reference (bf16 ``F.linear`` + fp32 ``log_softmax``).
+Interface kept: ``RestrictedLMHead(special_token_ids, enabled=True)``; the
+properties ``token_ids``, ``num_tokens``, ``ready``, ``per_codebook_ready``,
+``num_levels``, ``max_codebook_k``; ``codebook_k(level)``; ``bind(lm_weight)``
+(ids checked against the vocabulary, ``ValueError`` when out of range),
+``bind_codebook(sizes)`` (ignored unless the sizes add up to the bound
+rows), ``compute(hidden, lm_weight)``, ``compute_level(hidden, level)`` (past
+the last level: the whole restricted head) and ``compute_into(hidden,
+lm_weight, out)`` (needs a prior ``bind``, ``RuntimeError`` otherwise; never
+re-slices, so it can be graph-captured).  Results are fp32 log-probabilities
+over the restricted rows, in the order of ``special_token_ids``.
+
+Design here: the bound head is a ``_RowBlock`` -- the weight rows of the
+restricted ids (a zero-copy ``narrow`` when the ids are one contiguous run,
+a gathered copy otherwise), their ids on the device and, with ``fp8=True``,
+their per-row e4m3 codes and fp32 scales, quantised once at bind time.  A
+codebook level is a ``_RowBlock`` over a row range of the bound one (views
+of the same weight, codes and scales).  With ``fp8=True`` (this build's
+addition; the reference always runs a bf16 ``F.linear``) a call is three HIP
+kernels: per-token e4m3 quant of the hidden rows, the W8A8 GEMM with fp32
+logits, and a row-wise log_softmax written in place (or straight into
+``compute_into``'s ``out``).  With ``fp8=False`` it is the reference's bf16
+``F.linear`` + fp32 ``log_softmax``.
 """
 
 from __future__ import annotations
 
-from typing import List, Optional
+from dataclasses import dataclass
+from typing import List, Optional, Sequence, Tuple
 
 import torch
 import torch.nn.functional as F
@@ -21,158 +37,136 @@ from flashrec_amd.kernel.sglops import fp8_scaled_mm, log_softmax_f32, per_token
 from flashrec_amd.layers.linear import quantize_weight_fp8
 
 
-class RestrictedLMHead:
-    def __init__(
-        self,
-        special_token_ids: Optional[List[int]],
-        enabled: bool = True,
-        fp8: bool = False,
-    ):
-        self.ids = list(special_token_ids) if special_token_ids else None
-        self.enabled = bool(enabled and self.ids)
-        self.fp8 = bool(fp8)
-        self._token_ids: Optional[torch.Tensor] = None
-        self._weight: Optional[torch.Tensor] = None
-        self._q_weight: Optional[torch.Tensor] = None  # [K, N] column-major e4m3
-        self._q_scale: Optional[torch.Tensor] = None  # [N] fp32
-        self._level_weights: Optional[List[torch.Tensor]] = None
-        self._level_token_ids: Optional[List[torch.Tensor]] = None
-        self._level_offsets: Optional[List[int]] = None
-        self._codebook_sizes: Optional[List[int]] = None
+@dataclass
+class _RowBlock:
+    """Rows of the lm_head weight for a run of restricted ids."""
+
+    weight: torch.Tensor  # [n, hidden]
+    ids: torch.Tensor  # [n] int64, on the weight's device
+    codes: Optional[torch.Tensor] = None  # [n, hidden] e4m3 (fp8 heads)
+    scale: Optional[torch.Tensor] = None  # [n] fp32
 
     @property
+    def rows(self) -> int:
+        return int(self.weight.shape[0])
+
+    def sub(self, start: int, count: int) -> "_RowBlock":
+        def cut(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+            return None if t is None else t.narrow(0, start, count)
+
+        return _RowBlock(cut(self.weight), cut(self.ids), cut(self.codes), cut(self.scale))
+
+    def logprobs(self, hidden: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if self.codes is None:
+            logits = F.linear(hidden.to(dtype=self.weight.dtype), self.weight)
+            lp = F.log_softmax(logits.float(), dim=-1)
+            return lp if out is None else out.copy_(lp)
+        rows = hidden.reshape(-1, hidden.shape[-1])
+        a_codes, a_scale = per_token_quant_fp8(rows)
+        logits = fp8_scaled_mm(a_codes, self.codes.t(), a_scale, self.scale, torch.float32)
+        direct = (out is not None and out.dtype == torch.float32 and out.shape == logits.shape
+                  and out.stride(1) == 1 and out.device == logits.device)
+        if out is None or direct:
+            return log_softmax_f32(logits, out=logits if out is None else out)
+        return out.copy_(log_softmax_f32(logits, out=logits))
+
+
+def _one_run(ids: Sequence[int]) -> bool:
+    """True when the ids are lo, lo + 1, ..., lo + n - 1 (n > 1)."""
+    return len(ids) > 1 and all(b == a + 1 for a, b in zip(ids, ids[1:]))
+
+
+class RestrictedLMHead:
+    def __init__(self, special_token_ids: Optional[Sequence[int]], enabled: bool = True,
+                 fp8: bool = False):
+        self.ids: Optional[List[int]] = [int(i) for i in special_token_ids] if special_token_ids else None
+        self.enabled = bool(enabled) and self.ids is not None
+        self.fp8 = bool(fp8)
+        self._head: Optional[_RowBlock] = None
+        self._levels: List[_RowBlock] = []
+
+    # --- state -------------------------------------------------------------------
+    @property
     def token_ids(self) -> Optional[torch.Tensor]:
-        return self._token_ids
+        return None if self._head is None else self._head.ids
 
     @property
     def num_tokens(self) -> Optional[int]:
-        if self._token_ids is None:
-            return None
-        return int(self._token_ids.numel())
+        return None if self._head is None else self._head.rows
 
     @property
     def ready(self) -> bool:
-        return bool(self.enabled and self._weight is not None and self._token_ids is not None)
+        return self.enabled and self._head is not None
 
     @property
     def per_codebook_ready(self) -> bool:
-        return bool(self._level_weights is not None and len(self._level_weights) > 0)
+        return bool(self._levels)
 
     @property
     def num_levels(self) -> int:
-        return len(self._level_weights) if self._level_weights else 0
+        return len(self._levels)
 
     @property
     def max_codebook_k(self) -> int:
-        if not self._codebook_sizes:
-            return 0
-        return max(self._codebook_sizes)
+        return max((lv.rows for lv in self._levels), default=0)
 
     def codebook_k(self, level: int) -> int:
-        if not self._codebook_sizes or level < 0 or level >= len(self._codebook_sizes):
-            return 0
-        return self._codebook_sizes[level]
+        return self._levels[level].rows if 0 <= level < len(self._levels) else 0
 
-    def bind(self, lm_weight: torch.Tensor) -> None:
-        """Slice (and with fp8, quantise) the restricted rows once after weight load."""
-        if lm_weight is None:
-            return
-        self._ensure(lm_weight.device, lm_weight)
+    # --- binding -------------------------------------------------------------------
+    def _bound_to(self, lm_weight: torch.Tensor) -> bool:
+        return self._head is not None and self._head.weight.device == lm_weight.device
 
-    def bind_codebook(self, codebook_sizes: List[int]) -> None:
-        """Per-level zero-copy views of the bound slice (logits.py:66-90)."""
-        if self._weight is None or not self.enabled:
+    def bind(self, lm_weight: Optional[torch.Tensor]) -> None:
+        """Select (and with fp8 quantise) the restricted rows once after weight load."""
+        if lm_weight is None or not self.enabled or self._bound_to(lm_weight):
             return
-        total = sum(codebook_sizes)
-        if total != self._weight.shape[0]:
-            return
-        self._codebook_sizes = list(codebook_sizes)
-        self._level_weights = []
-        self._level_token_ids = []
-        self._level_offsets = []
-        offset = 0
         ids = self.ids or []
-        device = self._weight.device
-        for size in codebook_sizes:
-            self._level_weights.append(self._weight.narrow(0, offset, size))
-            self._level_token_ids.append(
-                torch.tensor(ids[offset : offset + size], dtype=torch.long, device=device)
-            )
-            self._level_offsets.append(offset)
-            offset += size
+        vocab = int(lm_weight.shape[0])
+        if min(ids) < 0 or max(ids) >= vocab:
+            raise ValueError(f"sid_token_range out of range for vocab {vocab}")
+        dev = lm_weight.device
+        id_t = torch.tensor(ids, dtype=torch.int64, device=dev)
+        rows = lm_weight.narrow(0, ids[0], len(ids)) if _one_run(ids) else lm_weight.index_select(0, id_t)
+        head = _RowBlock(rows, id_t)
+        if self.fp8:
+            head.codes, head.scale = quantize_weight_fp8(rows)
+        self._head = head
+        self._levels = []
 
-    def _ensure(self, device: torch.device, lm_weight: torch.Tensor) -> None:
-        """logits.py:92-116, plus the one-time fp8 quantisation of the slice."""
-        if not self.enabled:
+    def bind_codebook(self, codebook_sizes: Sequence[int]) -> None:
+        """One level per codebook, each a zero-copy row range of the bound head."""
+        if self._head is None or not self.enabled:
             return
-        if self._token_ids is None or self._token_ids.device != device:
-            vocab = int(lm_weight.shape[0])
-            ids = self.ids or []
-            if (not ids) or min(ids) < 0 or max(ids) >= vocab:
-                raise ValueError(f"sid_token_range out of range for vocab {vocab}")
-            self._token_ids = torch.tensor(ids, dtype=torch.long, device=device)
-            self._weight = None
-        if self._weight is None or self._weight.device != device:
-            ids = self.ids or []
-            lo, hi = int(ids[0]), int(ids[-1])
-            contiguous = (
-                len(ids) > 1
-                and hi - lo == len(ids) - 1
-                and all(b - a == 1 for a, b in zip(ids, ids[1:]))
-            )
-            if contiguous:
-                self._weight = lm_weight.narrow(0, lo, len(ids))
-            else:
-                self._weight = torch.index_select(lm_weight, 0, self._token_ids)
-            if self.fp8:
-                q, s = quantize_weight_fp8(self._weight)
-                self._q_weight = q.t()
-                self._q_scale = s
+        sizes = [int(n) for n in codebook_sizes]
+        if sum(sizes) != self._head.rows:
+            return
+        starts = [sum(sizes[:i]) for i in range(len(sizes))]
+        self._levels = [self._head.sub(s0, n) for s0, n in zip(starts, sizes)]
 
-    def _fp8_logprobs(self, hidden: torch.Tensor, lo: int, n: int,
-                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
-        assert self._q_weight is not None and self._q_scale is not None
-        qa, sa = per_token_quant_fp8(hidden)
-        w = self._q_weight.narrow(1, lo, n)
-        s = self._q_scale.narrow(0, lo, n)
-        logits = fp8_scaled_mm(qa, w, sa, s, torch.float32)
-        return log_softmax_f32(logits, out=logits if out is None else out)
-
-    def _restricted_logprobs(self, hidden: torch.Tensor) -> torch.Tensor:
-        if self.fp8:
-            return self._fp8_logprobs(hidden, 0, int(self._weight.shape[0]))
-        logits = F.linear(hidden.to(dtype=self._weight.dtype), self._weight)
-        return F.log_softmax(logits.float(), dim=-1)
-
-    def compute_level(self, hidden: torch.Tensor, level: int) -> tuple[torch.Tensor, torch.Tensor]:
-        """Per-codebook logprobs: GEMM only against the level's slice (logits.py:122-138)."""
-        weights = self._level_weights
-        ids = self._level_token_ids
-        if weights is None or ids is None or level < 0 or level >= len(weights):
-            if self._weight is None or self._token_ids is None:
-                raise RuntimeError("RestrictedLMHead.compute_level requires bind_codebook()")
-            return self._restricted_logprobs(hidden), self._token_ids
-        if self.fp8:
-            assert self._level_offsets is not None
-            lp = self._fp8_logprobs(hidden, self._level_offsets[level], int(weights[level].shape[0]))
-            return lp, ids[level]
-        w = weights[level]
-        logits = F.linear(hidden.to(dtype=w.dtype), w)
-        return F.log_softmax(logits.float(), dim=-1), ids[level]
-
-    def compute_into(self, hidden: torch.Tensor, lm_weight: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
-        """Write restricted logprobs into ``out`` [T, K] fp32 (logits.py:140-155)."""
-        del lm_weight
-        if self._weight is None or self._token_ids is None:
-            raise RuntimeError("RestrictedLMHead.compute_into requires bind()")
-        out.copy_(self._restricted_logprobs(hidden))
-        return out
-
-    def compute(self, hidden: torch.Tensor, lm_weight: torch.Tensor) -> tuple[torch.Tensor, Optional[torch.Tensor]]:
-        """Return (logprobs [T, K or V], candidate_token_ids or None) (logits.py:157-166)."""
-        device = hidden.device
-        self._ensure(device, lm_weight)
-        if self.enabled and self._weight is not None and self._token_ids is not None:
-            return self._restricted_logprobs(hidden), self._token_ids
+    # --- calls -------------------------------------------------------------------
+    def compute(self, hidden: torch.Tensor, lm_weight: torch.Tensor
+                ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+        """(logprobs ``[T, K]`` over the restricted ids, their ids), or over
+        the full vocabulary with ``None`` when the head is disabled."""
+        self.bind(lm_weight)
+        if self.ready:
+            return self._head.logprobs(hidden), self._head.ids
         logits = F.linear(hidden.to(dtype=lm_weight.dtype), lm_weight)
         return F.log_softmax(logits.float(), dim=-1), None
+
+    def compute_level(self, hidden: torch.Tensor, level: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Logprobs against one codebook level's rows only."""
+        if 0 <= level < len(self._levels):
+            block = self._levels[level]
+            return block.logprobs(hidden), block.ids
+        if self._head is None:
+            raise RuntimeError("RestrictedLMHead.compute_level requires bind_codebook()")
+        return self._head.logprobs(hidden), self._head.ids
+
+    def compute_into(self, hidden: torch.Tensor, lm_weight: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+        """Restricted logprobs written into ``out`` ``[T, K]`` fp32."""
+        del lm_weight  # already bound: nothing is sliced here
+        if self._head is None:
+            raise RuntimeError("RestrictedLMHead.compute_into requires bind()")
+        return self._head.logprobs(hidden, out=out)

@@ -46,43 +46,47 @@ int fr_per_token_quant_fp8(const void* x, int x_dtype, int64_t M, int64_t K, int
 int fr_quantize_weight_fp8(const void* w, int w_dtype, int64_t N, int64_t K, int64_t ldw,
                            void* q, float* s, void* stream);
 
-/* RMSNorm (optionally after `residual += x`, residual updated in place as
- * bf16) fused with per-token e4m3 quantisation.  x, residual, w: bf16.
- * residual may be NULL.  q: [M, H] e4m3 contiguous, s: [M] fp32.
+/* RMSNorm (optionally after `residual += x`, residual updated in place)
+ * fused with per-token e4m3 quantisation.  x, residual, w: all of x_dtype
+ * (FR_DTYPE_BF16 or FR_DTYPE_FP16; intermediates rounded to it as torch
+ * does); residual may be NULL.  q: [M, H] e4m3 contiguous, s: [M] fp32.
  * Replaces python/flashrec/kernel/rms_fp8.py:120-145
  * (rmsnorm_per_token_quant_fp8, fused_add_rmsnorm_per_token_quant_fp8). */
-int fr_rms_quant_fp8(const void* x, int64_t ldx, void* residual, int64_t ldr, const void* w,
-                     int64_t M, int64_t H, float eps, void* q, float* s, void* stream);
+int fr_rms_quant_fp8(const void* x, int x_dtype, int64_t ldx, void* residual, int64_t ldr,
+                     const void* w, int64_t M, int64_t H, float eps, void* q, float* s, void* stream);
 
-/* RMSNorm with bf16 output (out may alias x); with residual != NULL it is
- * fused_add_rmsnorm: residual = bf16(residual + x), out = rmsnorm(residual).
+/* RMSNorm with x_dtype output (out may alias x); with residual != NULL it is
+ * fused_add_rmsnorm: residual = round(residual + x), out = rmsnorm(residual).
+ * x_dtype: FR_DTYPE_BF16 or FR_DTYPE_FP16 (x, residual, w and out).
  * Replaces python/flashrec/kernel/sglops.py:33-45 (rmsnorm) and :48-61
  * (fused_add_rmsnorm). */
-int fr_rmsnorm(const void* x, int64_t ldx, void* residual, int64_t ldr, const void* w,
-               void* out, int64_t ldo, int64_t M, int64_t H, float eps, void* stream);
+int fr_rmsnorm(const void* x, int x_dtype, int64_t ldx, void* residual, int64_t ldr,
+               const void* w, void* out, int64_t ldo, int64_t M, int64_t H, float eps, void* stream);
 
-/* SiLU-and-mul over [M, 2d] bf16 rows (gate half first) fused with per-token
+/* SiLU-and-mul over [M, 2d] rows of x_dtype (FR_DTYPE_BF16 or FR_DTYPE_FP16;
+ * gate half first) fused with per-token
  * e4m3 quantisation: q [M, d] e4m3 contiguous, s [M] fp32.
  * Replaces python/flashrec/kernel/silu_fp8.py:85-119
  * (silu_and_mul_per_token_quant_fp8). */
-int fr_silu_quant_fp8(const void* x, int64_t ldx, int64_t M, int64_t d, void* q, float* s,
-                      void* stream);
+int fr_silu_quant_fp8(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t d, void* q,
+                      float* s, void* stream);
 
-/* SiLU-and-mul with bf16 output [M, d] (row stride ldo).
+/* SiLU-and-mul with x_dtype output [M, d] (row stride ldo).
  * Replaces python/flashrec/kernel/sglops.py:143-151 (silu_and_mul). */
-int fr_silu_and_mul(const void* x, int64_t ldx, void* out, int64_t ldo, int64_t M, int64_t d,
-                    void* stream);
+int fr_silu_and_mul(const void* x, int x_dtype, int64_t ldx, void* out, int64_t ldo, int64_t M,
+                    int64_t d, void* stream);
 
 /* W8A8 GEMM: out[m, n] = (sum_k a[m, k] b[k, n]) * scale_a[m] * scale_b[n]
  * (+ bias[n]).  a: [M, K] e4m3 row-major (row stride lda bytes);
  * b: [K, N] e4m3 column-major (column n at b + n * ldb); scale_a numel 1 or
- * M, scale_b numel 1 or N (fp32); bias: out_dtype [N] or NULL; out: [M, N]
+ * M, scale_b numel 1 or N (fp32); bias: out_dtype [N] or NULL, bias_numel its
+ * length (must be N when bias is given, else FR_EINVAL); out: [M, N]
  * of out_dtype (bf16, fp16 or fp32) with row stride ldo (elements).
  * Replaces python/flashrec/kernel/sglops.py:99-140 (fp8_scaled_mm). */
 int fr_fp8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
                      const float* scale_a, int64_t scale_a_numel, const float* scale_b,
-                     int64_t scale_b_numel, const void* bias, void* out, int64_t ldo, int64_t M,
-                     int64_t N, int64_t K, int out_dtype, void* stream);
+                     int64_t scale_b_numel, const void* bias, int64_t bias_numel, void* out,
+                     int64_t ldo, int64_t M, int64_t N, int64_t K, int out_dtype, void* stream);
 
 /* Per-head RMSNorm of q and k (weights q_weight, k_weight: bf16 [D]),
  * NeoX rotate-half RoPE from cos_sin_cache ([cache_rows, D] fp32: cos for
@@ -119,6 +123,29 @@ int fr_rope_inplace(void* q, int64_t sqt, int64_t sqh, void* k, int64_t skt, int
 int fr_store_kv_fp8(const void* k, int64_t skt, const void* v, int64_t svt, int src_dtype,
                     const int64_t* loc, void* k_cache, int64_t sck, void* v_cache, int64_t scv,
                     int64_t num_slots, int64_t T, int64_t row_dim, void* stream);
+
+/* KV store into a bf16 pool: bf16 k/v rows [T, row_dim] copied to
+ * k_cache/v_cache rows loc[t] (row strides in elements).  Slots outside
+ * [0, num_slots) are skipped.
+ * Replaces python/flashrec/kernel/sglops.py:207-222 (store_kv_cache) and
+ * python/flashrec/kvcache/pool.py:121-139 for a pool whose dtype matches the
+ * activations. */
+int fr_store_kv_bf16(const void* k, int64_t skt, const void* v, int64_t svt, const int64_t* loc,
+                     void* k_cache, int64_t sck, void* v_cache, int64_t scv, int64_t num_slots,
+                     int64_t T, int64_t row_dim, void* stream);
+
+/* RoPE + KV store for a bf16 pool: q [T, Hq, D] and k [T, Hk, D] rotated in
+ * place (as fr_rope_inplace), then the rotated k and the unchanged v written
+ * to k_cache/v_cache [slots, Hk, D] at loc[t] (strides in elements).  Slots
+ * outside [0, num_slots) and positions outside the cache are skipped.
+ * Replaces python/flashrec/kernel/sglops.py:154-204 (apply_rope_and_store_kv,
+ * the matching-dtype case). */
+int fr_rope_store_kv_bf16(void* q, int64_t sqt, int64_t sqh, void* k, int64_t skt, int64_t skh,
+                          const void* v, int64_t svt, int64_t svh, const int64_t* positions,
+                          const int64_t* loc, const float* cos_sin_cache, int64_t cache_rows,
+                          void* k_cache, int64_t sckp, int64_t sckh, void* v_cache, int64_t scvp,
+                          int64_t scvh, int64_t num_slots, int64_t T, int64_t Hq, int64_t Hk,
+                          int64_t D, void* stream);
 
 /* Paged attention over the e4m3 KV pool, page size 1, head dim 128.
  * q: [T, Hq, 128] bf16 (token / head strides sqt, sqh in elements);

@@ -54,10 +54,10 @@ def test_invalid_arguments_rejected_without_gpu():
     lib = _lib.load()
     # null pointers with a non-empty shape
     assert lib.fr_per_token_quant_fp8(None, 0, 4, 8, 8, None, None, None) == _lib.FR_EINVAL
-    assert lib.fr_fp8_scaled_mm(None, 16, None, 16, None, 1, None, 1, None, None, 4, 4, 4, 16, 0,
+    assert lib.fr_fp8_scaled_mm(None, 16, None, 16, None, 1, None, 1, None, 0, None, 4, 4, 4, 16, 0,
                                 None) == _lib.FR_EINVAL
     # negative sizes
-    assert lib.fr_silu_quant_fp8(None, 0, -1, 4, None, None, None) == _lib.FR_EINVAL
+    assert lib.fr_silu_quant_fp8(None, 0, 0, -1, 4, None, None, None) == _lib.FR_EINVAL
     # unsupported head dim
     args = [None] * 28
     args[25] = 256

@@ -109,22 +109,68 @@ def test_gemm_row_major_b_is_copied(dev):
     assert max_abs_rel(out, ref) < TOL
 
 
+def _all_rows_rel(out, qa, sa, qw, sw, chunk=1024):
+    """max |out - oracle| / max |oracle| over every row, the oracle evaluated
+    in row chunks (fp32 dequantised matmul)."""
+    out = out.cpu().float()
+    b = qw.float() * sw.reshape(-1, 1).float()  # [N, K]
+    err, peak = 0.0, 0.0
+    for r0 in range(0, out.shape[0], chunk):
+        a = qa[r0:r0 + chunk].float() * sa[r0:r0 + chunk].reshape(-1, 1).float()
+        ref = a @ b.t()
+        err = max(err, (out[r0:r0 + chunk] - ref).abs().max().item())
+        peak = max(peak, ref.abs().max().item())
+    return err / peak
+
+
 def test_gemm_config1_full_size_rows(dev):
-    """Config 1 at M=4096 (gate_up, K=2048, N=12288): every row of a seeded
-    sample of 96 rows against the oracle, plus the agreement of the full
-    output with the reference's literal torch._scaled_mm CPU branch on the
-    same rows."""
+    """Config 1 at M=4096 (gate_up, K=2048, N=12288, the headline shape):
+    every row against the oracle, plus agreement of a row sample with the
+    reference's literal torch._scaled_mm CPU branch."""
     x, gamma, eps = inputs.config0(m=4096)
     qa, sa = ops.rmsnorm_per_token_quant_fp8(x, gamma, eps)
     qw, sw = ops.quantize_weight_fp8(inputs.config1_weight())
     out = _run(dev, qa, sa, qw, sw)
-    rows = torch.randperm(4096, generator=torch.Generator().manual_seed(1))[:96]
-    ref = ops.fp8_scaled_mm(qa[rows], qw.t(), sa[rows], sw)
-    got = out.cpu()[rows]
-    assert max_abs_rel(got, ref) < TOL
-    lit = ops.fp8_scaled_mm_torch_cpu(qa[rows], qw.t(), sa[rows], sw, torch.bfloat16)
-    assert max_abs_rel(got, lit.float()) < TOL
     assert torch.isfinite(out).all()
+    rel = _all_rows_rel(out, qa, sa, qw, sw)
+    print(f"config1 M=4096 all rows: max-abs-normalised error {rel:.2e}")
+    assert rel < TOL
+    rows = torch.randperm(4096, generator=torch.Generator().manual_seed(1))[:64]
+    lit = ops.fp8_scaled_mm_torch_cpu(qa[rows], qw.t(), sa[rows], sw, torch.bfloat16)
+    assert max_abs_rel(out.cpu()[rows], lit.float()) < TOL
+
+
+def test_gemm_config1_m512_all_rows(dev):
+    """Config 1 at its primary size, M=512 (the 192x128 one-round tiles)."""
+    x, gamma, eps = inputs.config0(m=512)
+    qa, sa = ops.rmsnorm_per_token_quant_fp8(x, gamma, eps)
+    qw, sw = ops.quantize_weight_fp8(inputs.config1_weight())
+    out = _run(dev, qa, sa, qw, sw)
+    rel = _all_rows_rel(out, qa, sa, qw, sw)
+    print(f"config1 M=512 all rows: {rel:.2e}")
+    assert rel < TOL
+
+
+def test_gemm_config2_down_all_rows(dev):
+    """Config 2: SiLU->fp8 of the seeded [4096, 12288] input, then the down
+    GEMM (K=6144, N=2048) at exactly that shape, every row."""
+    x, w = inputs.config2()
+    qa, sa = ops.silu_and_mul_per_token_quant_fp8(x)
+    qw, sw = ops.quantize_weight_fp8(w)
+    out = _run(dev, qa, sa, qw, sw)
+    rel = _all_rows_rel(out, qa, sa, qw, sw)
+    print(f"config2 down 4096x2048x6144 all rows: {rel:.2e}")
+    assert rel < TOL
+
+
+@pytest.mark.parametrize("name,n,k", [("qkv", 4096, 2048), ("o", 2048, 2048)])
+def test_gemm_config4_shapes_all_rows(dev, name, n, k):
+    """The config-4 decode-step projections at their exact 4096-row shapes."""
+    qa, sa, qw, sw = _operands(4096, n, k, seed=n + 3 * k)
+    out = _run(dev, qa, sa, qw, sw)
+    rel = _all_rows_rel(out, qa, sa, qw, sw)
+    print(f"config4 {name} 4096x{n}x{k} all rows: {rel:.2e}")
+    assert rel < TOL
 
 
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32, torch.float16])

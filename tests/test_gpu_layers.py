@@ -147,3 +147,39 @@ def test_graph_capture_replays(dev):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {i} differs"
+
+
+def test_kv_pool_alloc_uploads_without_blocking(dev):
+    """alloc() stages ids in pinned memory and copies them asynchronously;
+    many allocations wrap the staging ring and every result stays intact."""
+    from flashrec_amd.kvcache.pool import TokenToKVPool
+
+    pool = TokenToKVPool(1, 1 << 17, 1, 8, torch.bfloat16, dev)
+    pool._upload.capacity = 1024  # small ring: forces wrap-around
+    got, want = [], []
+    for i in range(200):
+        n = 1 + (i * 37) % 300
+        ids = pool.alloc(n)
+        assert ids.device.type == "cuda" and ids.dtype == torch.int64
+        got.append(ids)
+        want.append(list(pool.last_alloc_cpu))
+    torch.cuda.synchronize()
+    for ids, w in zip(got, want):
+        assert ids.cpu().tolist() == w
+    flat = [x for w in want for x in w]
+    assert len(set(flat)) == len(flat) and 0 not in flat
+    pool.free(torch.cat(got))
+    assert pool.available_size() == (1 << 17) - 1
+
+
+def test_kv_pool_bf16_store(dev):
+    from flashrec_amd.kvcache.pool import TokenToKVPool
+
+    pool = TokenToKVPool(1, 32, 2, 64, torch.bfloat16, dev)
+    loc = pool.alloc(5)
+    k = torch.randn(5, 2, 64, dtype=torch.bfloat16, device=dev)
+    v = torch.randn(5, 2, 64, dtype=torch.bfloat16, device=dev)
+    pool.store(0, k, v, loc)
+    torch.cuda.synchronize()
+    assert torch.equal(pool.k[0][loc], k) and torch.equal(pool.v[0][loc], v)
+    assert (pool.k[0][0] == 0).all()

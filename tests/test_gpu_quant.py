@@ -209,3 +209,43 @@ def test_empty_batch(dev):
 
     q, s = per_token_quant_fp8(torch.empty(0, 2048, dtype=torch.bfloat16, device=dev))
     assert q.shape == (0, 2048) and s.shape == (0, 1)
+
+
+@pytest.mark.parametrize("m,h", [(512, 2048), (7, 100)])
+def test_fp16_rms_quant_and_residual(dev, m, h):
+    """fp16 activations (reference rms_fp8.py:86 takes x.dtype): intermediates
+    round to fp16 as the reference's CPU composition does."""
+    from flashrec_amd.kernel.rms_fp8 import (fused_add_rmsnorm_per_token_quant_fp8,
+                                             rmsnorm_per_token_quant_fp8)
+    from flashrec_amd.kernel.sglops import rmsnorm
+
+    g = torch.Generator().manual_seed(m + h)
+    x = torch.randn(m, h, generator=g).to(torch.float16)
+    r = torch.randn(m, h, generator=g).to(torch.float16)
+    w = (1.0 + 0.1 * torch.randn(h, generator=g)).to(torch.bfloat16)
+    q, s = rmsnorm_per_token_quant_fp8(x.to(dev), w.to(dev), 1e-6)
+    q_ref, s_ref = ops.rmsnorm_per_token_quant_fp8(x, w, 1e-6)
+    assert_fp8_parity(q, s, q_ref, s_ref, label=f"fp16 rms {m}x{h}")
+    rd = r.to(dev)
+    q, s, res = fused_add_rmsnorm_per_token_quant_fp8(x.to(dev), rd, w.to(dev), 1e-6)
+    q_ref, s_ref, res_ref = ops.fused_add_rmsnorm_per_token_quant_fp8(x, r, w, 1e-6)
+    assert res.dtype == torch.float16 and torch.equal(res.cpu(), res_ref)
+    assert_fp8_parity(q, s, q_ref, s_ref, label=f"fp16 add+rms {m}x{h}")
+    y = rmsnorm(x.to(dev), w.to(dev), 1e-6)
+    assert y.dtype == torch.float16
+    assert_bf16_parity(y, ops.rmsnorm(x, w, 1e-6))  # 16-bit patterns: same bar
+
+
+@pytest.mark.parametrize("m,two_d", [(64, 12288), (5, 100)])
+def test_fp16_silu_quant(dev, m, two_d):
+    from flashrec_amd.kernel.sglops import silu_and_mul
+    from flashrec_amd.kernel.silu_fp8 import silu_and_mul_per_token_quant_fp8
+
+    g = torch.Generator().manual_seed(two_d)
+    x = (3 * torch.randn(m, two_d, generator=g)).to(torch.float16)
+    q, s = silu_and_mul_per_token_quant_fp8(x.to(dev))
+    q_ref, s_ref = ops.silu_and_mul_per_token_quant_fp8(x)
+    assert_fp8_parity(q, s, q_ref, s_ref, label=f"fp16 silu {m}x{two_d}")
+    y = silu_and_mul(x.to(dev))
+    assert y.dtype == torch.float16
+    assert_bf16_parity(y, ops.silu_and_mul(x))

@@ -181,3 +181,77 @@ def test_out_of_range_slots_are_skipped(dev):
     c = codes(kc)
     assert (c[1] == 0x38).all()  # e4m3(1.0)
     assert (c[[0, 2, 3]] == 0).all()
+
+
+@pytest.mark.parametrize("hq,hk,d", [(16, 8, 128), (6, 2, 64)])
+def test_rope_and_store_kv_bf16_pool(dev, hq, hk, d):
+    """Matching-dtype fused path (reference sglops.py:154-204): q and k rotated
+    in place, the rotated k and the untouched v written to a bf16 pool; the
+    oracle is RoPE then the pool store (qwen3.py:108-128's unfused order).
+    (16, 8, 128) takes the vector kernel, (6, 2, 64) the generic one."""
+    from flashrec_amd.kernel.sglops import apply_rope_and_store_kv
+
+    t, slots = 37, 300
+    g = torch.Generator().manual_seed(53)
+    qkv = torch.randn(t, (hq + 2 * hk) * d, generator=g).to(torch.bfloat16)
+    q, k, v = qkv.split([hq * d, hk * d, hk * d], dim=-1)  # strided views, as in the model
+    cache = ops.cos_sin_cache(d, 512, 1e6)
+    pos = torch.randint(0, 512, (t,), generator=g)
+    loc = torch.randperm(slots - 1, generator=g)[:t] + 1
+    loc[5] = slots + 7  # out of range slot: skipped
+    qkv_d = qkv.to(dev)
+    qd, kd, vd = qkv_d.split([hq * d, hk * d, hk * d], dim=-1)
+    kc = torch.zeros(slots, hk, d, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    assert apply_rope_and_store_kv(pos.to(dev), qd, kd, vd, loc.to(dev), kc, vc, d, cache.to(dev))
+    torch.cuda.synchronize()
+
+    q_ref = ops.apply_rope(pos, q.reshape(t, hq, d), cache)
+    k_ref = ops.apply_rope(pos, k.reshape(t, hk, d), cache)
+    bits = lambda x: x.cpu().contiguous().view(torch.int16)  # noqa: E731
+    assert torch.equal(bits(qd).view(t, hq, d), bits(q_ref))
+    assert torch.equal(bits(kd).view(t, hk, d), bits(k_ref))
+    assert torch.equal(bits(vd), bits(v))  # v is not modified
+    kc_ref = torch.zeros(slots, hk, d, dtype=torch.bfloat16)
+    vc_ref = torch.zeros_like(kc_ref)
+    keep = loc < slots
+    ops.store_kv(kc_ref, vc_ref, loc[keep], k_ref[keep], v.reshape(t, hk, d)[keep])
+    assert torch.equal(bits(kc), bits(kc_ref))
+    assert torch.equal(bits(vc), bits(vc_ref))
+
+
+def test_rope_and_store_kv_declines_fp8_pool(dev):
+    """An fp8 pool with bf16 activations is not this path (the reference returns False too)."""
+    from flashrec_amd.kernel.sglops import apply_rope_and_store_kv
+
+    q = torch.zeros(2, 128, dtype=torch.bfloat16, device=dev)
+    kc = torch.zeros(4, 1, 128, dtype=torch.float8_e4m3fn, device=dev)
+    assert not apply_rope_and_store_kv(torch.zeros(2, dtype=torch.int64, device=dev), q, q.clone(),
+                                       q.clone(), torch.ones(2, dtype=torch.int64, device=dev), kc,
+                                       kc.clone(), 128, torch.zeros(8, 128, device=dev))
+
+
+def test_store_kv_cache_bf16_pool(dev):
+    from flashrec_amd.kernel.sglops import store_kv_cache
+
+    n, row, slots = 64, 4 * 96, 200
+    g = torch.Generator().manual_seed(59)
+    k = torch.randn(n, row, generator=g).to(torch.bfloat16)
+    v = torch.randn(n, row, generator=g).to(torch.bfloat16)
+    loc = torch.randperm(slots - 1, generator=g)[:n] + 1
+    kc = torch.zeros(slots, row, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    store_kv_cache(kc, vc, loc.to(dev), k.to(dev), v.to(dev))
+    kc_ref = torch.zeros(slots, 4, 96, dtype=torch.bfloat16)
+    vc_ref = torch.zeros_like(kc_ref)
+    ops.store_kv(kc_ref, vc_ref, loc, k, v)
+    assert torch.equal(kc.cpu().view(torch.int16), kc_ref.view(slots, row).view(torch.int16))
+    assert torch.equal(vc.cpu().view(torch.int16), vc_ref.view(slots, row).view(torch.int16))
+    # odd row width: the element-wise form
+    k3 = k[:, :37].contiguous()
+    kc3 = torch.zeros(slots, 37, dtype=torch.bfloat16, device=dev)
+    vc3 = torch.zeros_like(kc3)
+    store_kv_cache(kc3, vc3, loc.to(dev), k3.to(dev), k3.to(dev))
+    ref3 = torch.zeros(slots, 37, dtype=torch.bfloat16)
+    ref3[loc] = k3
+    assert torch.equal(kc3.cpu(), ref3) and torch.equal(vc3.cpu(), ref3)

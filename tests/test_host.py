@@ -75,3 +75,92 @@ def test_bench_refuses_multi_gpu():
     res = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"],
                          capture_output=True, text=True, timeout=120)
     assert res.returncode == 2 and "one GPU" in res.stderr
+
+
+def test_scaled_mm_rejects_short_bias():
+    """The GEMM epilogue reads bias[0..N): a shorter bias is refused before any launch."""
+    from flashrec_amd.kernel.sglops import fp8_scaled_mm
+
+    a = torch.zeros(4, 32, dtype=torch.float8_e4m3fn)
+    b = torch.zeros(8, 32, dtype=torch.float8_e4m3fn).t()
+    with pytest.raises(ValueError, match="bias"):
+        fp8_scaled_mm(a, b, torch.ones(4, 1), torch.ones(8), torch.bfloat16, bias=torch.zeros(7))
+
+
+def test_scaled_mm_abi_rejects_bias_length():
+    """fr_fp8_scaled_mm returns FR_EINVAL for a bias length other than N (no launch)."""
+    from flashrec_amd import _lib
+
+    lib = _lib.load()
+    # non-null (never dereferenced) pointers: the length check comes first
+    p = 4096
+    rc = lib.fr_fp8_scaled_mm(p, 32, p, 32, p, 1, p, 1, p, 7, p, 8, 4, 8, 32, 0, None)
+    assert rc == _lib.FR_EINVAL
+
+
+def test_log_softmax_rejects_mismatched_out():
+    from flashrec_amd.kernel.sglops import log_softmax_f32
+
+    logits = torch.zeros(4, 16)
+    for bad in (torch.zeros(4, 8), torch.zeros(4, 16, dtype=torch.float16), torch.zeros(16, 4).t()):
+        with pytest.raises(ValueError):
+            log_softmax_f32(logits, out=bad)
+
+
+def test_linear_rejects_wrong_bias_and_rows():
+    lin = Linear(8, 4)
+    with pytest.raises(ValueError):
+        lin.load(torch.randn(4, 8), bias=torch.zeros(3))
+    with pytest.raises(ValueError):
+        lin.load(torch.randn(5, 8))
+
+
+def test_linear_codes_move_with_module():
+    lin = Linear(16, 8)
+    lin.load(torch.zeros(8, 16, dtype=torch.float8_e4m3fn), weight_scale=torch.arange(8.0))
+    assert set(dict(lin.named_buffers())) == {"w_codes", "w_scale"}
+    lin = lin.to(torch.bfloat16)  # a float cast keeps the codes and scales as they are
+    assert lin._fp8_weight.dtype == torch.float8_e4m3fn and lin._fp8_scale.dtype == torch.float32
+    assert torch.equal(lin._fp8_scale, torch.arange(8.0))
+
+
+def test_kv_pool_free_and_realloc_order():
+    """LIFO reuse: the last freed ids come back first, in the order freed."""
+    from flashrec_amd.kvcache.pool import TokenToKVPool
+
+    pool = TokenToKVPool(1, 10, 1, 8, torch.bfloat16, torch.device("cpu"))
+    a = pool.alloc(4)
+    assert a.tolist() == [6, 7, 8, 9] and pool.last_alloc_cpu == [6, 7, 8, 9]
+    pool.free([7, 0, -1, 9])
+    assert pool.available_size() == 7
+    assert pool.alloc(2).tolist() == [7, 9]
+    assert pool.alloc(0).numel() == 0 and pool.last_alloc_cpu == []
+    assert pool.alloc(100) is None
+    with pytest.raises(TypeError):
+        TokenToKVPool(1, 4, 1, 8, torch.float16, torch.device("cpu"))
+
+
+def test_pinned_upload_ring_reuses_regions():
+    """The upload ring wraps and retires the copies whose regions it reuses (CPU-side logic)."""
+    from flashrec_amd.kvcache.pool import _PinnedUpload
+
+    class _Ev:
+        def __init__(self):
+            self.waited = False
+
+        def synchronize(self):
+            self.waited = True
+
+    up = _PinnedUpload(torch.device("cpu"), capacity=16)
+    up._host = torch.empty(16, dtype=torch.int64)
+    evs = []
+    for n in (6, 6, 3):
+        start = up._reserve(n)
+        ev = _Ev()
+        evs.append(ev)
+        up._inflight.append((start, start + n, ev))
+    assert [r[:2] for r in up._inflight] == [(0, 6), (6, 12), (12, 15)]
+    start = up._reserve(5)  # does not fit at 15: wraps to 0 and retires (0, 6) only
+    assert start == 0 and evs[0].waited and not evs[1].waited and not evs[2].waited
+    start = up._reserve(4)  # [5, 9) meets (6, 12)
+    assert start == 5 and evs[1].waited and not evs[2].waited

@@ -206,3 +206,25 @@ def test_inputs_are_seeded(cfg):
         assert all(torch.equal(x, y) for x, y in zip(a, b))
         loc = a[4]
         assert (loc > 0).all() and loc.unique().numel() == 64  # slot 0 never used, no collisions
+
+
+def test_fp16_rows_round_to_fp16():
+    """fp16 activations (accepted by the reference's fused ops, rms_fp8.py:86,
+    silu_fp8.py:79-82): the oracle's intermediates are fp16 roundings of the
+    float64 closed forms, and the residual is the fp16-rounded exact sum."""
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(8, 64, generator=g).to(torch.float16)
+    w = (1 + 0.1 * torch.randn(64, generator=g)).to(torch.bfloat16)
+    out = ops.rmsnorm(x, w, 1e-6)
+    assert out.dtype == torch.float16
+    xd = x.double()
+    ref = xd / torch.sqrt((xd * xd).mean(-1, keepdim=True) + 1e-6) * w.double()
+    assert ((out.double() - ref).abs() / ref.abs().clamp(min=1e-4)).max() < 2.0 ** -10
+    r = torch.randn(8, 64, generator=g).to(torch.float16)
+    _, res = ops.fused_add_rmsnorm(x, r, w, 1e-6)
+    assert torch.equal(res, (x.double() + r.double()).to(torch.float16))
+    s = (torch.randn(8, 64, generator=g) * 3).to(torch.float16)
+    out = ops.silu_and_mul(s).double()
+    gt, up = s[:, :32].double(), s[:, 32:].double()
+    ref = gt / (1 + torch.exp(-gt)) * up
+    assert ((out - ref).abs() / ref.abs().clamp(min=1e-3)).max() < 2.0 ** -9  # two fp16 roundings
