@@ -21,6 +21,8 @@ FR_OK = 0
 FR_EINVAL = 1
 FR_EUNSUPPORTED = 2
 FR_ELAUNCH = 3
+FR_ETOOLARGE = 4
+GENREC_NOALLOC_SCRATCH_BYTES = 4 << 20  # FR_GENREC_NOALLOC_SCRATCH_BYTES
 
 DTYPE_CODE = {
     torch.bfloat16: 0,
@@ -63,6 +65,14 @@ SIGNATURES = {
     "fr_genrec_scratch_bytes": [_I64, _I64, _I64],
     "fr_genrec_mask_topk_expand": [
         _P, _P, _P, _P, _P, _I64,  # outputs, scratch + bytes
+        _P, _P, _P, _P, _P,  # cum, top_logprobs, top_tokens, node_ids, allow_table
+        _P, _P, _P, _P, _P, _P,  # token_ids in/out, next_node, node_ids_out, do_expand, col
+        _I64, _I64, _I64, _I64,  # token_base, n_nodes, vsz, invalid_node
+        _I64, _I64, _I64, _I64, _I64,  # N, BW, C, K, L
+        _I32, _I32, _I32, _I32, _P,  # apply flags, next_node is int32, stream
+    ],
+    "fr_genrec_mask_topk_expand_noalloc": [
+        _P, _P, _P, _P,  # outputs
         _P, _P, _P, _P, _P,  # cum, top_logprobs, top_tokens, node_ids, allow_table
         _P, _P, _P, _P, _P, _P,  # token_ids in/out, next_node, node_ids_out, do_expand, col
         _I64, _I64, _I64, _I64,  # token_base, n_nodes, vsz, invalid_node

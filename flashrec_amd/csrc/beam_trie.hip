@@ -31,6 +31,8 @@
 //     way (in groups that fit LDS, each folded into a running top K), writes
 //     vals / parents / tokens / indices, then the expanded token rows and the
 //     advanced trie nodes.
+#include <mutex>
+
 #include "fr_common.h"
 
 namespace fr {
@@ -300,22 +302,28 @@ extern "C" int fr_genrec_scratch_bytes(int64_t N, int64_t BW, int64_t K) {
   return bytes > 0x7FFFFFFF ? -1 : static_cast<int>(bytes);
 }
 
-extern "C" int fr_genrec_mask_topk_expand(
+// Argument checks shared by both entry points; the scratch is checked by
+// each (caller's buffer, or the library's static one).
+static int genrec_check(float* out_vals, int64_t* out_parents, int64_t* out_tokens, int64_t* out_indices,
+                        const float* cum, const float* top_logprobs, const int64_t* top_tokens,
+                        const int32_t* col, int64_t N, int64_t BW, int64_t C, int64_t K, int64_t L) {
+  if (N < 0 || BW <= 0 || C <= 0 || K <= 0 || L < 0) return FR_EINVAL;
+  if (N == 0) return FR_OK;
+  if (!out_vals || !out_parents || !out_tokens || !out_indices || !cum || !top_logprobs || !top_tokens ||
+      !col)
+    return FR_EINVAL;
+  if (K > 1024 || K > BW * C || BW * C > 0x7FFFFFFF) return FR_EUNSUPPORTED;
+  return FR_OK;
+}
+
+static int genrec_launch(
     float* out_vals, int64_t* out_parents, int64_t* out_tokens, int64_t* out_indices, void* scratch,
-    int64_t scratch_bytes, const float* cum, const float* top_logprobs, const int64_t* top_tokens,
+    const float* cum, const float* top_logprobs, const int64_t* top_tokens,
     const int64_t* node_ids, const uint8_t* allow_table, const int64_t* token_ids_in,
     int64_t* token_ids_out, const void* next_node, int64_t* node_ids_out, const uint8_t* do_expand,
     const int32_t* col, int64_t token_base, int64_t n_nodes, int64_t vsz, int64_t invalid_node,
     int64_t N, int64_t BW, int64_t C, int64_t K, int64_t L, int apply_mask, int apply_expand,
     int apply_advance, int next_i32, void* stream) {
-  if (N < 0 || BW <= 0 || C <= 0 || K <= 0 || L < 0) return FR_EINVAL;
-  if (N == 0) return FR_OK;
-  if (!out_vals || !out_parents || !out_tokens || !out_indices || !scratch || !cum || !top_logprobs ||
-      !top_tokens || !col)
-    return FR_EINVAL;
-  if (K > 1024 || K > BW * C || BW * C > 0x7FFFFFFF) return FR_EUNSUPPORTED;
-  const int need = fr_genrec_scratch_bytes(N, BW, K);
-  if (need < 0 || scratch_bytes < need) return FR_EINVAL;
   if (apply_mask && node_ids && allow_table && n_nodes > 0 && vsz <= 0) return FR_EINVAL;
   if (apply_expand && (!token_ids_in || !token_ids_out || L <= 0)) return FR_EINVAL;
   if (apply_expand && token_ids_in == token_ids_out) return FR_EINVAL;  // rows gather from other rows
@@ -356,4 +364,70 @@ extern "C" int fr_genrec_mask_topk_expand(
   hipLaunchKernelGGL(genrec_slice_topk, dim3(static_cast<unsigned>(N * a.S)), dim3(256), 0, st, a);
   hipLaunchKernelGGL(genrec_request_topk_expand, dim3(static_cast<unsigned>(N)), dim3(1024), 0, st, a);
   return hipGetLastError() == hipSuccess ? FR_OK : FR_ELAUNCH;
+}
+
+extern "C" int fr_genrec_mask_topk_expand(
+    float* out_vals, int64_t* out_parents, int64_t* out_tokens, int64_t* out_indices, void* scratch,
+    int64_t scratch_bytes, const float* cum, const float* top_logprobs, const int64_t* top_tokens,
+    const int64_t* node_ids, const uint8_t* allow_table, const int64_t* token_ids_in,
+    int64_t* token_ids_out, const void* next_node, int64_t* node_ids_out, const uint8_t* do_expand,
+    const int32_t* col, int64_t token_base, int64_t n_nodes, int64_t vsz, int64_t invalid_node,
+    int64_t N, int64_t BW, int64_t C, int64_t K, int64_t L, int apply_mask, int apply_expand,
+    int apply_advance, int next_i32, void* stream) {
+  const int rc = genrec_check(out_vals, out_parents, out_tokens, out_indices, cum, top_logprobs, top_tokens,
+                              col, N, BW, C, K, L);
+  if (rc != FR_OK || N == 0) return rc;
+  if (!scratch) return FR_EINVAL;
+  const int need = fr_genrec_scratch_bytes(N, BW, K);
+  if (need < 0 || scratch_bytes < need) return FR_EINVAL;
+  return genrec_launch(out_vals, out_parents, out_tokens, out_indices, scratch, cum, top_logprobs,
+                       top_tokens, node_ids, allow_table, token_ids_in, token_ids_out, next_node,
+                       node_ids_out, do_expand, col, token_base, n_nodes, vsz, invalid_node, N, BW, C, K, L,
+                       apply_mask, apply_expand, apply_advance, next_i32, stream);
+}
+
+// ---- The same step with no allocation anywhere: the slice lists live in a
+// static device array of FR_GENREC_NOALLOC_SCRATCH_BYTES (every GPU the
+// library runs on holds its own copy until the process ends).  Its device
+// address is looked up once per device, with that device current; host code
+// never passes the array's name to a kernel (on the host that name is a
+// stand-in, not a device address).  The slice kernel writes every list entry
+// the request kernel reads, so nothing needs clearing between calls.  All
+// calls on one GPU share the array: calls that overlap on one GPU (other
+// streams, other threads) race.
+static __device__ __align__(256) uint64_t genrec_static_scratch[FR_GENREC_NOALLOC_SCRATCH_BYTES / 8];
+
+static void* genrec_static_scratch_ptr() {
+  static std::mutex mu;
+  static void* ptrs[kMaxDevices] = {};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (ptrs[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(genrec_static_scratch)) != hipSuccess) return nullptr;
+    ptrs[dev] = p;
+  }
+  return ptrs[dev];
+}
+
+extern "C" int fr_genrec_mask_topk_expand_noalloc(
+    float* out_vals, int64_t* out_parents, int64_t* out_tokens, int64_t* out_indices, const float* cum,
+    const float* top_logprobs, const int64_t* top_tokens, const int64_t* node_ids,
+    const uint8_t* allow_table, const int64_t* token_ids_in, int64_t* token_ids_out,
+    const void* next_node, int64_t* node_ids_out, const uint8_t* do_expand, const int32_t* col,
+    int64_t token_base, int64_t n_nodes, int64_t vsz, int64_t invalid_node, int64_t N, int64_t BW,
+    int64_t C, int64_t K, int64_t L, int apply_mask, int apply_expand, int apply_advance, int next_i32,
+    void* stream) {
+  const int rc = genrec_check(out_vals, out_parents, out_tokens, out_indices, cum, top_logprobs, top_tokens,
+                              col, N, BW, C, K, L);
+  if (rc != FR_OK || N == 0) return rc;
+  const int need = fr_genrec_scratch_bytes(N, BW, K);
+  if (need < 0 || need > FR_GENREC_NOALLOC_SCRATCH_BYTES) return FR_ETOOLARGE;
+  void* scratch = genrec_static_scratch_ptr();
+  if (scratch == nullptr) return FR_ELAUNCH;
+  return genrec_launch(out_vals, out_parents, out_tokens, out_indices, scratch, cum, top_logprobs,
+                       top_tokens, node_ids, allow_table, token_ids_in, token_ids_out, next_node,
+                       node_ids_out, do_expand, col, token_base, n_nodes, vsz, invalid_node, N, BW, C, K, L,
+                       apply_mask, apply_expand, apply_advance, next_i32, stream);
 }

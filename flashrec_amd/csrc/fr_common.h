@@ -15,6 +15,14 @@
 #define FR_EINVAL 1      // bad pointer / size / stride
 #define FR_EUNSUPPORTED 2  // shape the kernels do not handle (caller falls back)
 #define FR_ELAUNCH 3     // HIP launch error
+#define FR_ETOOLARGE 4   // request exceeds a fixed capacity (no-allocation entry points)
+
+// static device scratch of fr_genrec_mask_topk_expand_noalloc, per GPU
+#define FR_GENREC_NOALLOC_SCRATCH_BYTES (4 << 20)
+
+namespace fr {
+constexpr int kMaxDevices = 64;  // per-device tables of host-side state
+}  // namespace fr
 
 #define FR_DTYPE_BF16 0
 #define FR_DTYPE_FP16 1

@@ -23,6 +23,7 @@ extern "C" {
 #define FR_EINVAL 1        /* null pointer, negative size, bad stride/scale size */
 #define FR_EUNSUPPORTED 2  /* valid request the kernels do not handle; caller falls back */
 #define FR_ELAUNCH 3       /* HIP reported a launch error */
+#define FR_ETOOLARGE 4     /* request exceeds a fixed capacity (no-allocation entry points) */
 
 #define FR_DTYPE_BF16 0
 #define FR_DTYPE_FP16 1
@@ -209,6 +210,26 @@ int fr_genrec_mask_topk_expand(float* out_vals, int64_t* out_parents, int64_t* o
                                int64_t n_nodes, int64_t vsz, int64_t invalid_node, int64_t N,
                                int64_t BW, int64_t C, int64_t K, int64_t L, int apply_mask,
                                int apply_expand, int apply_advance, int next_i32, void* stream);
+
+/* fr_genrec_mask_topk_expand with no allocation anywhere, for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * that forbid hipMalloc).  No counterpart in the reference.  Same arguments
+ * and results without the scratch buffer: the slice lists go to a static
+ * device array of FR_GENREC_NOALLOC_SCRATCH_BYTES per GPU, held until the
+ * process ends (its address is looked up on the first call on each device).
+ * Returns FR_ETOOLARGE when fr_genrec_scratch_bytes(N, BW, K) exceeds that
+ * size (config 4, 8 x 512 beams with K = 512, needs 1.05 MB).  All calls on
+ * one GPU share the array: calls that overlap on one GPU race. */
+#define FR_GENREC_NOALLOC_SCRATCH_BYTES (4 << 20)
+int fr_genrec_mask_topk_expand_noalloc(float* out_vals, int64_t* out_parents, int64_t* out_tokens,
+                                       int64_t* out_indices, const float* cum, const float* top_logprobs,
+                                       const int64_t* top_tokens, const int64_t* node_ids,
+                                       const uint8_t* allow_table, const int64_t* token_ids_in,
+                                       int64_t* token_ids_out, const void* next_node, int64_t* node_ids_out,
+                                       const uint8_t* do_expand, const int32_t* col, int64_t token_base,
+                                       int64_t n_nodes, int64_t vsz, int64_t invalid_node, int64_t N,
+                                       int64_t BW, int64_t C, int64_t K, int64_t L, int apply_mask,
+                                       int apply_expand, int apply_advance, int next_i32, void* stream);
 
 /* Per-row top-C of fp32 scores x [R, V] (row stride ldx): out_vals [R, C]
  * sorted descending (NaN above +inf, equal scores by ascending index),

@@ -99,3 +99,22 @@ def test_fused_ops_raise_on_cpu():
 def test_product_does_not_import_oracle():
     for p in (ROOT / "flashrec_amd").rglob("*.py"):
         assert "oracle" not in re.findall(r"^\s*(?:from|import)\s+(\w+)", p.read_text(), flags=re.M), p
+
+
+def test_header_constants_match_the_library_sources():
+    """Status codes and capacities are defined in the public header and in the
+    kernels' common header: both, and the Python binding, must agree."""
+    from flashrec_amd import _lib
+
+    def defines(path):
+        text = (ROOT / path).read_text()
+        return {m.group(1): m.group(2).strip() for m in re.finditer(r"#define (FR_\w+) (.+?)(?:\s*/[*/].*)?$",
+                                                                     text, re.M)}
+
+    pub = defines("include/flashrec_amd.h")
+    kern = defines("flashrec_amd/csrc/fr_common.h")
+    for name in ("FR_OK", "FR_EINVAL", "FR_EUNSUPPORTED", "FR_ELAUNCH", "FR_ETOOLARGE",
+                 "FR_GENREC_NOALLOC_SCRATCH_BYTES", "FR_DTYPE_BF16", "FR_DTYPE_E4M3"):
+        assert pub[name] == kern[name], name
+    assert int(pub["FR_ETOOLARGE"]) == _lib.FR_ETOOLARGE
+    assert eval(pub["FR_GENREC_NOALLOC_SCRATCH_BYTES"]) == _lib.GENREC_NOALLOC_SCRATCH_BYTES
