@@ -656,10 +656,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   // of the step on the 4096-row gate_up, qkv, down and o shapes, M = 512 and
   // fp32 outputs: 3/8 best or within 1 % on each, 2-7 % over waiting at the
   // start (0 restores that).
-#ifndef FR_GEMM_MIDW
-#define FR_GEMM_MIDW 3
-#endif
-  constexpr int MW = FR_GEMM_MIDW * NMF / 8;
+  constexpr int MW = 3 * NMF / 8;
   // refill loads of the same step issued before that point
   constexpr int kEarly = [] {
     int n = 0;
@@ -795,20 +792,12 @@ static int num_cus() {
   return cached[dev];
 }
 
-#ifndef FR_GEMM_RB_256x256
-#define FR_GEMM_RB_256x256 128
-#endif
-#ifndef FR_GEMM_RB_256x128
-#define FR_GEMM_RB_256x128 128
-#endif
-#ifndef FR_GEMM_RB_128x128
-#define FR_GEMM_RB_128x128 128
-#endif
-
-// Bytes of K per LDS row for a tile shape.
+// Bytes of K per LDS row: 128 for every tile shape (each direct-to-LDS load
+// then covers whole 128-byte lines; 64-byte rows measured slower on every
+// shape).
 template <int BN, int BM>
 constexpr int tile_rb() {
-  return BN == 256 && BM == 256 ? FR_GEMM_RB_256x256 : BN >= 192 ? FR_GEMM_RB_256x128 : FR_GEMM_RB_128x128;
+  return 128;
 }
 // Ring slots: the deepest ring that fits next to the scale buffers and the
 // epilogue staging (32 x 128 bytes per wave, or 32 x 64 where that buys a

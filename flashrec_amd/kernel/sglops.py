@@ -113,6 +113,25 @@ def per_token_quant_fp8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     return q, s
 
 
+def _mfma_operands(a: torch.Tensor, b: torch.Tensor, m: int, n: int, k: int):
+    """Operands the MFMA kernel takes: rows of a multiple of 16 bytes, 16-byte
+    aligned, K a multiple of 16.  Anything else is repacked here, with K
+    zero-padded (zeros add nothing to the products), instead of leaving it to
+    the library's scalar fallback kernel (a per-output VALU loop)."""
+    lda = a.stride(0) if m > 1 else k
+    ldb = b.stride(1) if n > 1 else k
+    ok = (k % 16 == 0 and lda % 16 == 0 and ldb % 16 == 0 and a.data_ptr() % 16 == 0
+          and b.data_ptr() % 16 == 0)
+    if ok or k == 0:
+        return a, b, k
+    k16 = (k + 15) // 16 * 16
+    a16 = torch.zeros((m, k16), dtype=torch.uint8, device=a.device)
+    a16[:, :k] = a.view(torch.uint8)
+    b16 = torch.zeros((n, k16), dtype=torch.uint8, device=b.device)
+    b16[:, :k] = b.t().view(torch.uint8)
+    return a16.view(a.dtype), b16.view(b.dtype).t(), k16
+
+
 @torch.compiler.disable
 def fp8_scaled_mm(
     a_fp8: torch.Tensor,
@@ -138,6 +157,7 @@ def fp8_scaled_mm(
     b = b_fp8
     if not (b.stride(0) == 1 and (n <= 1 or b.stride(1) >= k)):
         b = b.t().contiguous().t()  # column-major copy
+    a, b, k = _mfma_operands(a, b, m, n, k)
     sa = scale_a.reshape(-1).to(device=a.device, dtype=torch.float32).contiguous()
     sb = scale_b.reshape(-1).to(device=a.device, dtype=torch.float32).contiguous()
     if sa.numel() not in (1, m) or sb.numel() not in (1, n):

@@ -83,6 +83,10 @@ int fr_silu_and_mul(const void* x, int x_dtype, int64_t ldx, void* out, int64_t 
  * M, scale_b numel 1 or N (fp32); bias: out_dtype [N] or NULL, bias_numel its
  * length (must be N when bias is given, else FR_EINVAL); out: [M, N]
  * of out_dtype (bf16, fp16 or fp32) with row stride ldo (elements).
+ * Fast (MFMA) path: K, lda and ldb multiples of 16, a and b 16-byte aligned,
+ * each operand spanning < 2 GiB; anything else runs a scalar kernel, one
+ * thread per output, orders of magnitude slower (the Python wrapper repacks
+ * such operands, zero-padding K, so it never takes that path).
  * Replaces python/flashrec/kernel/sglops.py:99-140 (fp8_scaled_mm). */
 int fr_fp8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
                      const float* scale_a, int64_t scale_a_numel, const float* scale_b,

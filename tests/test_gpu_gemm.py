@@ -91,10 +91,42 @@ def test_gemm_per_tensor_scales(dev):
     assert max_abs_rel(out, ref) < TOL
 
 
-def test_gemm_scalar_path_odd_k(dev):
-    """K not a multiple of 16 takes the scalar kernel; same result bar."""
-    qa, sa, qw, sw = _operands(9, 70, 40, seed=8)
+@pytest.mark.parametrize("m,n,k", [(9, 70, 40), (300, 520, 1000), (64, 256, 2056)])
+def test_gemm_odd_k_is_padded_for_mfma(dev, m, n, k):
+    """K not a multiple of 16: the wrapper zero-pads K and runs the MFMA kernel."""
+    qa, sa, qw, sw = _operands(m, n, k, seed=8 + k)
     out = _run(dev, qa, sa, qw, sw, out_dtype=torch.float32)
+    ref = ops.fp8_scaled_mm(qa, qw.t(), sa, sw)
+    # fp32 outputs: only the order of the scaling against the sum differs
+    assert max_abs_rel(out, ref) < 1e-4
+
+
+def test_gemm_unaligned_views_are_repacked(dev):
+    """Operand views at odd byte offsets / row strides reach the MFMA kernel as aligned copies."""
+    from flashrec_amd.kernel.sglops import fp8_scaled_mm
+
+    qa, sa, qw, sw = _operands(33, 96, 256, seed=12)
+    wide = torch.zeros(33, 256 + 3, dtype=torch.uint8, device=dev)
+    wide[:, 3:] = qa.view(torch.uint8).to(dev)
+    a_view = wide[:, 3:].view(torch.float8_e4m3fn)  # row stride 259, data at +3 bytes
+    out = fp8_scaled_mm(a_view, qw.to(dev).t(), sa.to(dev), sw.to(dev), torch.float32)
+    ref = ops.fp8_scaled_mm(qa, qw.t(), sa, sw)
+    assert max_abs_rel(out, ref) < 1e-4
+
+
+def test_gemm_scalar_kernel_through_the_c_abi(dev):
+    """A C caller passing K % 16 != 0 gets the library's scalar kernel (the
+    Python wrapper never sends it there); same result."""
+    from flashrec_amd import _lib
+
+    m, n, k = 9, 70, 40
+    qa, sa, qw, sw = _operands(m, n, k, seed=8)
+    a, w, s_a, s_w = qa.to(dev), qw.to(dev), sa.to(dev).reshape(-1), sw.to(dev)
+    out = torch.empty(m, n, dtype=torch.float32, device=dev)
+    rc = _lib.load().fr_fp8_scaled_mm(a.data_ptr(), k, w.data_ptr(), k, s_a.data_ptr(), m, s_w.data_ptr(), n,
+                                      None, 0, out.data_ptr(), n, m, n, k, 2,
+                                      torch.cuda.current_stream(dev).cuda_stream)
+    assert rc == _lib.FR_OK
     ref = ops.fp8_scaled_mm(qa, qw.t(), sa, sw)
     assert max_abs_rel(out, ref) < 1e-5
 
