@@ -79,6 +79,9 @@ SIGNATURES = {
         _I64, _I64, _I64, _I64, _I64,  # N, BW, C, K, L
         _I32, _I32, _I32, _I32, _P,  # apply flags, next_node is int32, stream
     ],
+    "fr_trie_mask_candidates": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F32, _P],
+    "fr_trie_advance_nodes": [_P, _P, _P, _P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P],
+    "fr_beam_expand_token_ids": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
     "fr_row_topk": [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P],
     "fr_paged_attention_fp8": [
         _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,  # q, k_cache, v_cache + strides

@@ -232,3 +232,186 @@ def row_topk(
          tokens.data_ptr(),
          stream_of(scores))
     return vals, idx, tokens
+
+
+# ---------------------------------------------------------------------------
+# The rest of the reference module's interface (beam_trie.py:82-229, 302-353,
+# 633-690): the unfused trie steps that search/trie.py and search/state.py
+# call, the aliasing helpers the scheduler uses for its ping-pong stacks, and
+# the graph-capture entry into caller-owned buffers.
+
+tensors_alias = _same  # same storage, dtype, device, shape and strides (beam_trie.py:302-310)
+
+
+def row_aliases_stack(row: Optional[torch.Tensor], stacked_row: torch.Tensor) -> bool:
+    return row is not None and tensors_alias(row, stacked_row)
+
+
+def rows_alias_stack(rows, stacked: torch.Tensor) -> bool:
+    """Whether ``rows[i]`` is exactly ``stacked[i]`` for every row (beam_trie.py:319-325)."""
+    return len(rows) == int(stacked.shape[0]) and all(
+        row_aliases_stack(r, stacked[i]) for i, r in enumerate(rows))
+
+
+def pick_pingpong_stack(ws: GenrecFusedWorkspace, name: str, rows, shape: tuple, dtype: torch.dtype,
+                        device) -> torch.Tensor:
+    """The workspace plane already holding ``rows`` (no copy), else plane ``a``
+    with the rows copied in (beam_trie.py:328-352)."""
+    planes = ws.pair(name, shape, dtype, device)
+    for plane in planes:
+        if rows_alias_stack(rows, plane):
+            return plane
+    a = planes[0]
+    for i in range(int(shape[0])):
+        if rows[i] is None:
+            raise ValueError(f"{name}: missing row {i}")
+        a[i].copy_(rows[i])
+    return a
+
+
+def try_load_beam_trie() -> bool:
+    """True when the HIP kernels can run here (a GPU and the library)."""
+    if not torch.cuda.is_available():
+        return False
+    try:
+        load()
+    except Exception:
+        return False
+    return True
+
+
+def _u8_table(table: torch.Tensor) -> torch.Tensor:
+    t = table.view(torch.uint8) if table.dtype == torch.bool else table
+    if t.dtype != torch.uint8:
+        raise TypeError(f"allow_table must be bool or uint8, got {table.dtype}")
+    return t.contiguous()
+
+
+def trie_mask_candidates(scores: torch.Tensor, cand_tokens: torch.Tensor, node_ids: torch.Tensor,
+                         allow_table: torch.Tensor, token_base: int, out: Optional[torch.Tensor] = None,
+                         neg_inf: float = float("-inf")) -> torch.Tensor:
+    """``scores[r, c]`` where token ``cand_tokens[r, c]`` is allowed under trie
+    node ``node_ids[r]``, ``neg_inf`` elsewhere (beam_trie.py:82-117)."""
+    require_device(scores, cand_tokens, node_ids, allow_table)
+    if scores.dim() != 2 or tuple(cand_tokens.shape) != tuple(scores.shape):
+        raise ValueError("scores and cand_tokens must be [rows, cols] of one shape")
+    rows, cols = int(scores.shape[0]), int(scores.shape[1])
+    if int(node_ids.numel()) != rows:
+        raise ValueError(f"node_ids has {node_ids.numel()} entries for {rows} rows")
+    sc = scores.to(torch.float32).contiguous()
+    out = torch.empty_like(sc) if out is None else out
+    if out.dtype != torch.float32 or tuple(out.shape) != (rows, cols) or not out.is_contiguous():
+        raise ValueError("out must be a contiguous fp32 tensor of the scores' shape")
+    allow = _u8_table(allow_table)
+    call("fr_trie_mask_candidates", out.data_ptr(), sc.data_ptr(), _i64(cand_tokens).data_ptr(),
+         _i64(node_ids.reshape(-1)).data_ptr(), allow.data_ptr(), rows, cols, int(allow.shape[0]),
+         int(allow.shape[1]), int(token_base), float(neg_inf), stream_of(sc))
+    return out
+
+
+def _advance(node_ids, parents, tokens, next_node, token_base, invalid_node, out, batch, rows, picks):
+    require_device(node_ids, parents, tokens, next_node)
+    if next_node.dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"next_node must be int32 or int64, got {next_node.dtype}")
+    nxt = next_node.contiguous()
+    par = _i64(parents.to(device=node_ids.device).reshape(batch, picks))
+    tok = _i64(tokens.to(device=node_ids.device).reshape(batch, picks))
+    if out is None:
+        out = torch.empty((batch, picks), dtype=torch.int64, device=node_ids.device)
+    if out.dtype != torch.int64 or out.numel() != batch * picks or not out.is_contiguous():
+        raise ValueError("out must be a contiguous int64 tensor with one entry per pick")
+    call("fr_trie_advance_nodes", out.data_ptr(), _i64(node_ids).data_ptr(), par.data_ptr(), tok.data_ptr(),
+         nxt.data_ptr(), int(nxt.dtype == torch.int32), batch, rows, picks, int(nxt.shape[0]),
+         int(nxt.shape[1]), int(token_base), int(invalid_node), stream_of(node_ids))
+    return out
+
+
+def trie_advance_nodes(node_ids: torch.Tensor, parents: torch.Tensor, tokens: torch.Tensor,
+                       next_node: torch.Tensor, token_base: int, invalid_node: int,
+                       out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Each pick's new trie node: its parent beam's node stepped on its token
+    (beam_trie.py:120-162); ``node_ids`` [rows], ``parents`` / ``tokens`` [picks]."""
+    picks = int(parents.numel())
+    res = _advance(node_ids, parents, tokens, next_node, token_base, invalid_node,
+                   None if out is None else out.view(1, -1), 1, int(node_ids.numel()), picks)
+    return res.view(picks) if out is None else out
+
+
+def trie_advance_nodes_batched(node_ids: torch.Tensor, parents: torch.Tensor, tokens: torch.Tensor,
+                               next_node: torch.Tensor, token_base: int, invalid_node: int,
+                               out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Per request: ``node_ids`` [n, bw], ``parents`` / ``tokens`` [n, k]
+    (beam_trie.py:165-192); a 1-D ``node_ids`` is the unbatched form."""
+    if node_ids.dim() == 1:
+        return trie_advance_nodes(node_ids, parents, tokens, next_node, token_base, invalid_node, out)
+    n, bw = int(node_ids.shape[0]), int(node_ids.shape[1])
+    picks = int(parents.numel()) // max(n, 1)
+    res = _advance(node_ids, parents, tokens, next_node, token_base, invalid_node, out, n, bw, picks)
+    return res.view(n, picks)
+
+
+def beam_expand_token_ids(token_ids: torch.Tensor, parents: torch.Tensor, new_tokens: torch.Tensor, col: int,
+                          out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Token rows of the picks: row ``parents[p]`` of ``token_ids`` [rows,
+    width] with column ``col`` set to ``new_tokens[p]`` (beam_trie.py:195-228;
+    ``col == width`` appends the column, as the reference's PyTorch branch
+    does).  int64 tokens."""
+    require_device(token_ids, parents, new_tokens)
+    if token_ids.dim() != 2:
+        raise ValueError("token_ids must be [rows, width]")
+    rows, width = int(token_ids.shape[0]), int(token_ids.shape[1])
+    col = int(col)
+    if col < 0 or col > width:
+        raise IndexError(f"col {col} outside 0..{width}")
+    par = _i64(parents.to(device=token_ids.device).reshape(-1))
+    picks = int(par.numel())
+    toks = _i64(new_tokens.to(device=token_ids.device).reshape(-1))
+    if int(toks.numel()) != picks:
+        raise ValueError("one new token per parent")
+    src = _i64(token_ids)
+    shape = (picks, max(width, col + 1))
+    if out is None:
+        out = torch.empty(shape, dtype=torch.int64, device=token_ids.device)
+    if out.dtype != torch.int64 or tuple(out.shape) != shape or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous int64 tensor of shape {shape}")
+    if picks and rows == 0:
+        raise IndexError("no token rows to gather from")
+    call("fr_beam_expand_token_ids", out.data_ptr(), src.data_ptr(), par.data_ptr(), toks.data_ptr(), rows, width,
+         picks, col, stream_of(src))
+    return out if token_ids.dtype == torch.int64 else out.to(token_ids.dtype)
+
+
+def call_genrec_cuda(out_vals, out_parents, out_tokens, out_indices, scratch, cum, top_logprobs, top_tokens,
+                     node_in, allow_u8, tok_in, tok_out, next_node, node_out, do_exp, token_base: int,
+                     invalid_node: int, col_t, apply_mask: int = 1, apply_expand: int = 1,
+                     apply_advance: int = 1) -> bool:
+    """The fused step into caller-owned buffers, graph-capture safe
+    (beam_trie.py:633-684): K is ``out_vals.shape[1]``.  The caller's
+    ``scratch`` (the reference sizes it [N, BW * C] fp32) is used when it is
+    large enough; otherwise the library's static per-device scratch
+    (``fr_genrec_mask_topk_expand_noalloc``).  Returns False when neither fits."""
+    lib = load()
+    n, bw = int(cum.shape[0]), int(cum.shape[1])
+    c = int(top_logprobs.shape[2])
+    k = int(out_vals.shape[1])
+    width = int(tok_in.shape[-1]) if tok_in is not None else 0
+    allow = _u8_table(allow_u8) if allow_u8 is not None else None
+    next_i32 = int(next_node is not None and next_node.dtype == torch.int32)
+
+    def p(t):
+        return 0 if t is None else t.data_ptr()
+
+    args = (p(cum), p(top_logprobs), p(top_tokens), p(node_in), p(allow), p(tok_in), p(tok_out), p(next_node),
+            p(node_out), p(do_exp), p(col_t), int(token_base), 0 if allow is None else int(allow.shape[0]),
+            0 if allow is None else int(allow.shape[1]), int(invalid_node), n, bw, c, k, width,
+            int(apply_mask), int(apply_expand), int(apply_advance), next_i32, stream_of(cum))
+    head = (p(out_vals), p(out_parents), p(out_tokens), p(out_indices))
+    need = int(lib.fr_genrec_scratch_bytes(n, bw, k))
+    if need < 0:
+        return False
+    have = 0 if scratch is None else int(scratch.numel()) * scratch.element_size()
+    if have >= need:
+        rc = lib.fr_genrec_mask_topk_expand(*head, scratch.data_ptr(), have, *args)
+    else:
+        rc = lib.fr_genrec_mask_topk_expand_noalloc(*head, *args)
+    return rc == 0

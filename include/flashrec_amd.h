@@ -215,6 +215,40 @@ int fr_genrec_mask_topk_expand(float* out_vals, int64_t* out_parents, int64_t* o
                                int64_t BW, int64_t C, int64_t K, int64_t L, int apply_mask,
                                int apply_expand, int apply_advance, int next_i32, void* stream);
 
+/* The beam-search trie steps one at a time (the unfused path of
+ * python/flashrec/search/trie.py:480-580 and search/state.py).  Candidate
+ * rule and transition as in fr_genrec_mask_topk_expand; integer selection,
+ * bit-exact.
+ *
+ * fr_trie_mask_candidates: out[r, c] = scores[r, c] if the token
+ * cand_tokens[r, c] is allowed under node_ids[r] (allow_table [n_nodes, vsz]
+ * uint8, tokens relative to token_base), else neg_inf; scores, out [rows,
+ * cols] fp32 (out may alias scores).
+ * Replaces python/flashrec/kernel/beam_trie.py:82-117 (trie_mask_candidates). */
+int fr_trie_mask_candidates(float* out, const float* scores, const int64_t* cand_tokens, const int64_t* node_ids,
+                            const uint8_t* allow_table, int64_t rows, int64_t cols, int64_t n_nodes, int64_t vsz,
+                            int64_t token_base, float neg_inf, void* stream);
+
+/* fr_trie_advance_nodes: for each of `batch` planes, out[b, i] =
+ * step(node_ids[b, clamp(parents[b, i], 0, rows - 1)], tokens[b, i]) over
+ * next_node [n_nodes, vsz] (int32 when next_i32, else int64); node_ids [batch,
+ * rows], parents / tokens / out [batch, picks] int64.
+ * Replaces python/flashrec/kernel/beam_trie.py:120-162 (trie_advance_nodes,
+ * batch = 1) and :165-192 (trie_advance_nodes_batched). */
+int fr_trie_advance_nodes(int64_t* out, const int64_t* node_ids, const int64_t* parents, const int64_t* tokens,
+                          const void* next_node, int next_i32, int64_t batch, int64_t rows, int64_t picks,
+                          int64_t n_nodes, int64_t vsz, int64_t token_base, int64_t invalid_node,
+                          void* stream);
+
+/* fr_beam_expand_token_ids: out[p, :] = token_ids[clamp(parents[p], 0, rows -
+ * 1), :] with column col set to new_tokens[p]; token_ids [rows, width], out
+ * [picks, max(width, col + 1)] int64 (col == width appends one column, col >
+ * width is FR_EINVAL).
+ * Replaces python/flashrec/kernel/beam_trie.py:195-228 (beam_expand_token_ids). */
+int fr_beam_expand_token_ids(int64_t* out, const int64_t* token_ids, const int64_t* parents,
+                             const int64_t* new_tokens, int64_t rows, int64_t width, int64_t picks, int64_t col,
+                             void* stream);
+
 /* fr_genrec_mask_topk_expand with no allocation anywhere, for callers that
  * cannot allocate device memory (code under HIP graph capture, serving loops
  * that forbid hipMalloc).  No counterpart in the reference.  Same arguments

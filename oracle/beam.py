@@ -114,3 +114,52 @@ def row_topk(x: torch.Tensor, k: int, cand_ids: Optional[torch.Tensor] = None):
     tokens = cand_ids.long()[idx] if cand_ids is not None else idx.clone()
     shape = tuple(x.shape[:-1]) + (k,)
     return vals.reshape(shape), idx.reshape(shape), tokens.reshape(shape)
+
+
+# ---------------------------------------------------------------- unfused steps
+def trie_mask_candidates(scores, cand_tokens, node_ids, allow_table, token_base, neg_inf=NEG_INF):
+    """python/flashrec/kernel/beam_trie.py:105-117 (PyTorch branch): scores
+    [rows, cols] kept where cand_ok(node_ids[row], token), else neg_inf."""
+    allow = allow_table.bool()
+    n_nodes, vsz = allow.shape
+    rel = cand_tokens.long() - int(token_base)
+    in_range = (rel >= 0) & (rel < vsz)
+    node = node_ids.long().reshape(-1, 1).expand_as(rel)
+    if n_nodes > 0 and vsz > 0:
+        ok = allow[node.clamp(0, n_nodes - 1), rel.clamp(0, vsz - 1)] & in_range
+    else:
+        ok = torch.zeros_like(in_range)
+    ok = ok | (node < 0)
+    return scores.float().masked_fill(~ok, neg_inf)
+
+
+def trie_advance_nodes(node_ids, parents, tokens, next_node, token_base, invalid_node):
+    """python/flashrec/kernel/beam_trie.py:145-162 (PyTorch branch), one
+    plane: new node of each pick = transition(node_ids[clamp(parent)], token)."""
+    n_nodes, vsz = next_node.shape
+    par = parents.long().reshape(-1).clamp(0, max(int(node_ids.numel()) - 1, 0))
+    old = node_ids.long().reshape(-1)[par]
+    rel = tokens.long().reshape(-1) - int(token_base)
+    in_range = (rel >= 0) & (rel < vsz) & (n_nodes > 0)
+    if n_nodes > 0 and vsz > 0:
+        nxt = next_node.long()[old.clamp(0, n_nodes - 1), rel.clamp(0, vsz - 1)]
+    else:
+        nxt = torch.zeros_like(old)
+    nxt = torch.where(in_range, nxt, torch.full_like(nxt, int(invalid_node)))
+    return torch.where(old < 0, old, nxt)
+
+
+def trie_advance_nodes_batched(node_ids, parents, tokens, next_node, token_base, invalid_node):
+    """python/flashrec/kernel/beam_trie.py:165-192: one plane per request."""
+    return torch.stack([trie_advance_nodes(node_ids[r], parents[r], tokens[r], next_node, token_base, invalid_node)
+                        for r in range(int(node_ids.shape[0]))])
+
+
+def beam_expand_token_ids(token_ids, parents, new_tokens, col):
+    """python/flashrec/kernel/beam_trie.py:218-228 (PyTorch branch)."""
+    par = parents.long().reshape(-1).clamp(0, max(int(token_ids.shape[0]) - 1, 0))
+    rows = token_ids[par].clone()
+    if col >= rows.shape[1]:
+        rows = torch.nn.functional.pad(rows, (0, 1))
+    rows[:, col] = new_tokens.reshape(-1).to(rows.dtype)
+    return rows

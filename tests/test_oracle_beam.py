@@ -122,3 +122,49 @@ def test_row_topk_ties_nan_and_signed_zero_by_hand():
     assert vals[0, 2:].tolist() == [inf, 1.0, 1.0, 0.0, -0.0, -0.0, -inf]
     _, idx3, _ = beam.row_topk(x, 3)
     assert idx3.tolist() == [[3, 7, 6]]
+
+
+def test_unfused_mask_matches_scalar_rule_and_hand_case():
+    """trie_mask_candidates against cand_ok() element by element (random
+    tables with out-of-table tokens, unconstrained nodes, NaN scores), and a
+    hand-worked case."""
+    g = torch.Generator().manual_seed(21)
+    rows, cols, n_nodes, vsz, base = 12, 9, 7, 10, 100
+    scores = torch.randn(rows, cols, generator=g)
+    scores[0, 0] = float("nan")
+    toks = base + torch.randint(-2, vsz + 2, (rows, cols), generator=g)
+    nodes = torch.randint(-1, n_nodes + 2, (rows,), generator=g)  # -1 and past the table
+    allow = torch.rand(n_nodes, vsz, generator=g) < 0.5
+    got = beam.trie_mask_candidates(scores, toks, nodes, allow, base)
+    for r in range(rows):
+        for c in range(cols):
+            ok = beam.cand_ok(int(nodes[r]), int(toks[r, c]), allow, base)
+            want = scores[r, c] if ok else torch.tensor(float("-inf"))
+            assert torch.equal(got[r, c], want) or (torch.isnan(want) and torch.isnan(got[r, c]))
+    # hand case: node 1 allows relative tokens 0 and 2 only
+    allow2 = torch.tensor([[1, 1, 1], [1, 0, 1]], dtype=torch.bool)
+    out = beam.trie_mask_candidates(torch.ones(1, 4), torch.tensor([[5, 6, 7, 9]]), torch.tensor([1]), allow2, 5)
+    assert out.tolist() == [[1.0, float("-inf"), 1.0, float("-inf")]]
+
+
+def test_unfused_advance_and_expand_match_scalar_rules():
+    g = torch.Generator().manual_seed(22)
+    bw, picks, n_nodes, vsz, base, invalid = 6, 10, 5, 8, 50, 99
+    nodes = torch.randint(-1, n_nodes, (bw,), generator=g)
+    parents = torch.randint(-2, bw + 2, (picks,), generator=g)  # clamped
+    toks = base + torch.randint(-1, vsz + 1, (picks,), generator=g)
+    nxt = torch.randint(0, n_nodes, (n_nodes, vsz), generator=g)
+    got = beam.trie_advance_nodes(nodes, parents, toks, nxt, base, invalid)
+    for i in range(picks):
+        p = min(max(int(parents[i]), 0), bw - 1)
+        assert int(got[i]) == beam.transition(int(nodes[p]), int(toks[i]), nxt, base, invalid)
+    batched = beam.trie_advance_nodes_batched(nodes.view(2, 3), parents.view(2, 5).clamp(0, 2), toks.view(2, 5),
+                                              nxt, base, invalid)
+    for r in range(2):
+        assert torch.equal(batched[r], beam.trie_advance_nodes(nodes.view(2, 3)[r], parents.view(2, 5)[r].clamp(0, 2),
+                                                               toks.view(2, 5)[r], nxt, base, invalid))
+    ti = torch.arange(12).view(3, 4)
+    out = beam.beam_expand_token_ids(ti, torch.tensor([2, 0, 5]), torch.tensor([70, 71, 72]), 1)
+    assert out.tolist() == [[8, 70, 10, 11], [0, 71, 2, 3], [8, 72, 10, 11]]
+    out = beam.beam_expand_token_ids(ti, torch.tensor([1]), torch.tensor([9]), 4)  # appends a column
+    assert out.tolist() == [[4, 5, 6, 7, 9]]
