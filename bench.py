@@ -108,7 +108,7 @@ def _decode_step_case(dev):
     """Config 4: the 28-layer decode step at 4096 beam rows (8 requests x 512
     beams over a 128-token shared prompt), one HIP-graph replay per step;
     its paged attention kernel timed alone over the same batch."""
-    from flashrec_amd.attention import paged_attention
+    from flashrec_amd.attention import paged_attention, paged_attention_quant_fp8
     from flashrec_amd.decode_step import Qwen3FP8DecodeStep, Qwen3Shape
 
     shape = Qwen3Shape()
@@ -155,6 +155,17 @@ def _decode_step_case(dev):
     flops = 4.0 * rows * shape.q_heads * m.seq_len * shape.head_dim
     out["config4_decode_attention"] = {"ms": round(ms_a, 5), "TFLOP/s": round(flops / (ms_a * 1e-3) / 1e12, 1),
                                        "bound": "bf16 MFMA + gather latency", "rows": rows, "kv_len": m.seq_len}
+    codes = torch.empty(rows, shape.q_heads * shape.head_dim, dtype=torch.float8_e4m3fn, device=dev)
+    scales = torch.empty(rows, 1, dtype=torch.float32, device=dev)
+
+    def step_q(_i):
+        paged_attention_quant_fp8(q, k0, v0, p["indices"], p["start"], p["len"], shape.head_dim ** -0.5,
+                                  group_prefix=p["group_prefix"], out=codes, out_scale=scales)
+
+    ms_aq = _graph_timed(step_q, 1)
+    out["config4_decode_attention_quant"] = {
+        "ms": round(ms_aq, 5), "rows": rows, "kv_len": m.seq_len,
+        "what": "attention fused with the o projection's per-token e4m3 quant (the decode step's path)"}
     del m
     torch.cuda.empty_cache()
     return out

@@ -88,6 +88,11 @@ SIGNATURES = {
         _I64, _P, _P, _P,  # num_slots, kv_indices, kv_start, kv_len
         _P, _I64, _I64, _I64, _I64, _I64, _I64, _F32, _P, _P,  # out + strides, T, Hq, Hk, D, scale, plan, stream
     ],
+    "fr_paged_attention_quant_fp8": [
+        _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,  # q, k_cache, v_cache + strides
+        _I64, _P, _P, _P,  # num_slots, kv_indices, kv_start, kv_len
+        _P, _I64, _P, _I64, _I64, _I64, _I64, _F32, _P, _P,  # codes, ldq, scales, T, Hq, Hk, D, scale, plan, stream
+    ],
     "fr_paged_attention_plan_size": [_I64, _I64, _I64],
     "fr_paged_attention_plan": [_P, _P, _P, _I64, _I64, _I64, _P, _P],
 }

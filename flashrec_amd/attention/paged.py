@@ -13,11 +13,11 @@ only its output and can be captured.
 
 from __future__ import annotations
 
-from typing import Dict, List, Optional
+from typing import Dict, List, Optional, Tuple
 
 import torch
 
-from flashrec_amd._lib import call, load, require_device, stream_of
+from flashrec_amd._lib import Unsupported, call, load, require_device, stream_of
 
 
 class AttentionBackend:
@@ -163,6 +163,18 @@ class AttentionBackend:
                                self.scale, group_prefix=self._plan.get("group_prefix"))
 
 
+    @torch.compiler.disable
+    def forward_quant_fp8(self, q: torch.Tensor, layer_id: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Attention over the stored KV fused with the o projection's per-token
+        e4m3 quant: (codes [T, Hq * D], scales [T, 1]).  The new KV must be
+        stored already (the fused QK-norm/RoPE/KV write does it)."""
+        if self._plan is None:
+            raise RuntimeError("AttentionBackend.forward_quant_fp8 before prepare() (kv_indices required)")
+        return paged_attention_quant_fp8(q, self.kv_pool.k_cache(layer_id), self.kv_pool.v_cache(layer_id),
+                                         self._plan["indices"], self._plan["start"], self._plan["len"],
+                                         self.scale, group_prefix=self._plan.get("group_prefix"))
+
+
 def plan_size(T: int, hq: int, hk: int) -> int:
     """Entries of an attention plan for T query tokens (groups of 32 / (hq / hk))."""
     n = int(load().fr_paged_attention_plan_size(int(T), int(hq), int(hk)))
@@ -188,17 +200,7 @@ def attention_plan(kv_indices: torch.Tensor, kv_start: torch.Tensor, kv_len: tor
     return out
 
 
-def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
-                    kv_indices: torch.Tensor, kv_start: torch.Tensor, kv_len: torch.Tensor,
-                    scale: float, out: Optional[torch.Tensor] = None,
-                    group_prefix: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """softmax(q k^T * scale) v over each query token's slot list.
-
-    q: [T, Hq, 128] bf16 (unit inner stride); k_cache / v_cache: [slots, Hk,
-    128] float8_e4m3fn; kv_indices / kv_start / kv_len: int32 on the device.
-    group_prefix: the plan of ``attention_plan`` for the same slot lists, or
-    None (each call then finds the shared prefixes itself).
-    """
+def _check_attention_inputs(q, k_cache, v_cache, kv_indices, kv_start, kv_len):
     require_device(q, k_cache, v_cache, kv_indices, kv_start, kv_len)
     if q.dtype != torch.bfloat16:
         raise TypeError("paged_attention takes bf16 queries")
@@ -215,6 +217,60 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
         raise ValueError("caches need a unit inner stride")
     if kv_start.numel() < T or kv_len.numel() < T:
         raise ValueError("one kv_start / kv_len entry per query token")
+    return T, Hq, D, slots, Hk
+
+
+def paged_attention_quant_fp8(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                              kv_indices: torch.Tensor, kv_start: torch.Tensor, kv_len: torch.Tensor,
+                              scale: float, group_prefix: Optional[torch.Tensor] = None,
+                              out: Optional[torch.Tensor] = None, out_scale: Optional[torch.Tensor] = None
+                              ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``per_token_quant_fp8(paged_attention(...).reshape(T, -1))`` in one
+    kernel: the o projection's e4m3 input ``[T, Hq * D]`` and its scales
+    ``[T, 1]`` (qwen3.py:131-134 -> linear.py:118-151), bit-for-bit the two
+    steps' result.  Head layouts the fused kernel does not take (more than 8
+    kv heads, 8 query heads per kv head) run the two steps."""
+    T, Hq, D, slots, Hk = _check_attention_inputs(q, k_cache, v_cache, kv_indices, kv_start, kv_len)
+    if out is None:
+        out = torch.empty(T, Hq * D, dtype=torch.float8_e4m3fn, device=q.device)
+    if out_scale is None:
+        out_scale = torch.empty(T, 1, dtype=torch.float32, device=q.device)
+    if (out.dtype != torch.float8_e4m3fn or out.dim() != 2 or out.shape[0] != T or out.shape[1] != Hq * D
+            or out.stride(1) != 1):
+        raise ValueError("out must be [T, Hq * D] float8_e4m3fn with a unit inner stride")
+    if out_scale.dtype != torch.float32 or out_scale.numel() != T or not out_scale.is_contiguous():
+        raise ValueError("out_scale must hold T contiguous fp32 values")
+    require_device(out, out_scale)
+    try:
+        call("fr_paged_attention_quant_fp8",
+             q.data_ptr(), q.stride(0), q.stride(1),
+             k_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1),
+             v_cache.data_ptr(), v_cache.stride(0), v_cache.stride(1),
+             slots, kv_indices.data_ptr(), kv_start.data_ptr(), kv_len.data_ptr(),
+             out.data_ptr(), out.stride(0), out_scale.data_ptr(),
+             T, Hq, Hk, D, float(scale), 0 if group_prefix is None else group_prefix.data_ptr(), stream_of(q))
+    except Unsupported:
+        from flashrec_amd.kernel.sglops import per_token_quant_fp8
+
+        o = paged_attention(q, k_cache, v_cache, kv_indices, kv_start, kv_len, scale, group_prefix=group_prefix)
+        codes, s = per_token_quant_fp8(o.reshape(T, Hq * D))
+        out.copy_(codes)
+        out_scale.copy_(s.reshape(out_scale.shape))
+    return out, out_scale
+
+
+def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                    kv_indices: torch.Tensor, kv_start: torch.Tensor, kv_len: torch.Tensor,
+                    scale: float, out: Optional[torch.Tensor] = None,
+                    group_prefix: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """softmax(q k^T * scale) v over each query token's slot list.
+
+    q: [T, Hq, 128] bf16 (unit inner stride); k_cache / v_cache: [slots, Hk,
+    128] float8_e4m3fn; kv_indices / kv_start / kv_len: int32 on the device.
+    group_prefix: the plan of ``attention_plan`` for the same slot lists, or
+    None (each call then finds the shared prefixes itself).
+    """
+    T, Hq, D, slots, Hk = _check_attention_inputs(q, k_cache, v_cache, kv_indices, kv_start, kv_len)
     if out is None:
         out = torch.empty(T, Hq, D, dtype=torch.bfloat16, device=q.device)
     call("fr_paged_attention_fp8",

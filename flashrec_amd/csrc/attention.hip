@@ -75,9 +75,11 @@ __device__ __forceinline__ void e4m3x16_to_f32(const u32x4& w, float* f) {
 // chunks of 8 * NP: scores of a chunk stay in registers (pass 1, K), then the
 // chunk is folded into a running max / sum / accumulator (pass 2, V) in the
 // exp2 domain (q carries scale * log2(e)); the 8 key groups' partial sums
-// are merged once at the end.
+// are merged once at the end.  Head kh * NREP + r's output row goes to
+// op0 + r * ohs (global memory, or the LDS staging of the quantizing kernel).
 template <int NREP, int NP>
-__device__ __forceinline__ void attend_token(const AttnArgs& a, int64_t t, int kh, int lane) {
+__device__ __forceinline__ void attend_token(const AttnArgs& a, int64_t t, int kh, int lane, uint16_t* op0,
+                                             int64_t ohs) {
   const int kg = lane >> 3;       // key group
   const int d0 = (lane & 7) * 16;  // first of this lane's 16 dims
 
@@ -206,7 +208,7 @@ __device__ __forceinline__ void attend_token(const AttnArgs& a, int64_t t, int k
       o0[i] = pack_bf16x2(acc[r][2 * i] * inv, acc[r][2 * i + 1] * inv);
       o1[i] = pack_bf16x2(acc[r][8 + 2 * i] * inv, acc[r][8 + 2 * i + 1] * inv);
     }
-    uint16_t* op = a.out + t * a.sot + (kh * NREP + r) * a.soh + d0;
+    uint16_t* op = op0 + r * ohs + d0;
     *reinterpret_cast<u32x4*>(op) = o0;
     *reinterpret_cast<u32x4*>(op + 8) = o1;
   }
@@ -331,17 +333,14 @@ constexpr int kVRow = 288;  // LDS bytes per staged V row: 256 + 32 (bank spread
 template <int NREP>
 constexpr bool kSeparateTokenKernel = NREP >= 8;
 
-template <int NREP>
-__global__ __launch_bounds__(256, 2) void paged_attn_grouped_d128(AttnArgs a) {
+// One (group, kv head kh) item on one wave; vs is the wave's 32 x kVRow
+// bytes of LDS.  STAGE: the 32 query rows' outputs go to vs (row n = query
+// column n, bf16 at byte 2 * dim) instead of a.out, for the quantizing
+// kernel below.
+template <int NREP, bool STAGE>
+__device__ __forceinline__ void grouped_item(const AttnArgs& a, uint8_t* vs, int64_t group, int kh, int lane) {
   constexpr int TOK = 32 / NREP;  // tokens per group
-  __shared__ __attribute__((aligned(16))) uint8_t lds[4 * 32 * kVRow];
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + wave;
-  const int64_t group = item / a.Hk;
-  const int kh = static_cast<int>(item - group * a.Hk);
   const int64_t t0 = group * TOK;
-  if (t0 >= a.T) return;
   const int n = lane & 31;  // query column (and key row when loading)
   const int h = lane >> 5;  // half: dims 64h .. 64h + 63
   // this lane's query and key token: t0 + n / NREP (head kh * NREP + n % NREP).
@@ -366,11 +365,17 @@ __global__ __launch_bounds__(256, 2) void paged_attn_grouped_d128(AttnArgs a) {
   if (a.gp ? a.gp[group] == 0 : !group_shares_block<TOK>(a, t0, lane)) {
     if constexpr (!kSeparateTokenKernel<NREP>) {
       const int ntok = static_cast<int>(min<int64_t>(TOK, a.T - t0));
-      for (int tt = 0; tt < ntok; ++tt) attend_token<NREP, 16 / NREP>(a, t0 + tt, kh, lane);
+      for (int tt = 0; tt < ntok; ++tt) {
+        if constexpr (STAGE)
+          attend_token<NREP, 16 / NREP>(a, t0 + tt, kh, lane, reinterpret_cast<uint16_t*>(vs + tt * NREP * kVRow),
+                                        kVRow / 2);
+        else
+          attend_token<NREP, 16 / NREP>(a, t0 + tt, kh, lane, a.out + (t0 + tt) * a.sot + kh * NREP * a.soh,
+                                        a.soh);
+      }
     }
     return;
   }
-  uint8_t* vs = lds + wave * (32 * kVRow);
 
   // ---- shared slot prefix of the group's tokens: from the plan, or found here
   const int32_t P32 = a.gp ? a.gp[group] : group_prefix32<TOK>(a, t0, lane);
@@ -538,7 +543,8 @@ __global__ __launch_bounds__(256, 2) void paged_attn_grouped_d128(AttnArgs a) {
   const float lt = l + __shfl_xor(l, 32, 64);
   if (!qok) return;
   const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-  uint16_t* op = a.out + tq * a.sot + (kh * NREP + n % NREP) * a.soh;
+  uint16_t* op = STAGE ? reinterpret_cast<uint16_t*>(vs + n * kVRow)
+                       : a.out + tq * a.sot + (kh * NREP + n % NREP) * a.soh;
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
@@ -548,6 +554,81 @@ __global__ __launch_bounds__(256, 2) void paged_attn_grouped_d128(AttnArgs a) {
       w[1] = pack_bf16x2(O[mt][4 * j + 2] * inv, O[mt][4 * j + 3] * inv);
       *reinterpret_cast<u32x2*>(op + 32 * mt + 8 * j + 4 * h) = w;
     }
+}
+
+template <int NREP>
+__global__ __launch_bounds__(256, 2) void paged_attn_grouped_d128(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[4 * 32 * kVRow];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+  const int64_t group = item / a.Hk;
+  const int kh = static_cast<int>(item - group * a.Hk);
+  if (group * (32 / NREP) >= a.T) return;
+  grouped_item<NREP, false>(a, lds + wave * (32 * kVRow), group, kh, lane);
+}
+
+// Attention fused with the per-token e4m3 quant of its output (the o_proj
+// input, linear.py:118-151 -> sglops.py:84-96): one workgroup per group of
+// 32 / NREP tokens, wave w on kv head w (Hk <= 8, NREP < 8).  Each wave
+// stages its 32 bf16 output rows in its LDS region; after a barrier, wave w
+// takes tokens w, w + 8, ...: the token's Hq x 128 bf16 values (4 heads per
+// pass, 8 dims per lane), row amax, scale = amax / 448 and the codes, in the
+// row kernels' arithmetic (quant8_e4m3).  The codes are bit-for-bit what
+// paged_attn_grouped_d128 followed by the per-token quant writes.
+template <int NREP>
+__global__ __launch_bounds__(512, 1) void paged_attn_grouped_quant_d128(AttnArgs a, uint8_t* qout, int64_t ldq,
+                                                                        float* qscale) {
+  constexpr int TOK = 32 / NREP;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[8 * 32 * kVRow];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t group = blockIdx.x;
+  const int64_t t0 = group * TOK;
+  if (t0 >= a.T) return;
+  if (wave < a.Hk) grouped_item<NREP, true>(a, lds + wave * (32 * kVRow), group, wave, lane);
+  __syncthreads();
+  const int ntok = static_cast<int>(min<int64_t>(TOK, a.T - t0));
+  const int hq = static_cast<int>(a.Hq);
+  const int hl = lane >> 4;       // head inside a pass of 4
+  const int dl = (lane & 15) * 8;  // first of this lane's 8 dims
+  for (int tt = wave; tt < ntok; tt += 8) {
+    u32x4 w[8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      const int head = 4 * p + hl;
+      w[p] = u32x4{0, 0, 0, 0};
+      if (head < hq) {
+        const uint8_t* src = lds + (head / NREP) * (32 * kVRow) + (tt * NREP + head % NREP) * kVRow + 2 * dl;
+        w[p] = *reinterpret_cast<const u32x4*>(src);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        amax = maxnan(amax, __builtin_fabsf(__uint_as_float(w[p][i] << 16)));
+        amax = maxnan(amax, __builtin_fabsf(__uint_as_float(w[p][i] & 0xFFFF0000u)));
+      }
+    }
+    amax = maxnan(wave_maxnan(amax), kAmaxFloor);
+    const float scale = amax / kFp8Max;
+    const int64_t t = t0 + tt;
+    if (lane == 0) qscale[t] = scale;
+    const bool finite = amax < 3.0e38f;
+    const float r = 1.0f / scale;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      const int head = 4 * p + hl;
+      if (head < hq) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[2 * i] = __uint_as_float(w[p][i] << 16);
+          v[2 * i + 1] = __uint_as_float(w[p][i] & 0xFFFF0000u);
+        }
+        *reinterpret_cast<u32x2*>(qout + t * ldq + head * 128 + dl) = quant8_e4m3(v, scale, r, finite);
+      }
+    }
+  }
 }
 
 // The groups grouped_d128 leaves: one workgroup per group; its waves (8, or
@@ -568,7 +649,11 @@ __global__ __launch_bounds__(64 * token_waves<NREP>()) void paged_attn_tokens_d1
   const int ntok = static_cast<int>(min<int64_t>(TOK, a.T - t0));
   const int pairs = ntok * static_cast<int>(a.Hk);
   for (int p = wave; p < pairs; p += token_waves<NREP>())
-    attend_token<NREP, NP>(a, t0 + p / a.Hk, static_cast<int>(p % a.Hk), lane);
+  {
+    const int64_t t = t0 + p / a.Hk;
+    const int kh = static_cast<int>(p % a.Hk);
+    attend_token<NREP, NP>(a, t, kh, lane, a.out + t * a.sot + kh * NREP * a.soh, a.soh);
+  }
 }
 
 // One launch, or two for NREP >= 8 (the token path in a kernel of its own):
@@ -589,23 +674,30 @@ static hipError_t launch_grouped(const AttnArgs& a, hipStream_t st) {
 
 using namespace fr;
 
-extern "C" int fr_paged_attention_fp8(const void* q, int64_t sqt, int64_t sqh, const void* k_cache,
-                                      int64_t skp, int64_t skh, const void* v_cache, int64_t svp,
-                                      int64_t svh, int64_t num_slots, const int32_t* kv_indices,
-                                      const int32_t* kv_start, const int32_t* kv_len, void* out,
-                                      int64_t sot, int64_t soh, int64_t T, int64_t Hq, int64_t Hk,
-                                      int64_t D, float scale, const int32_t* group_prefix,
-                                      void* stream) {
+template <int NREP>
+static hipError_t launch_grouped_quant(const AttnArgs& a, uint8_t* qout, int64_t ldq, float* qs, hipStream_t st) {
+  const int64_t groups = (a.T + 32 / NREP - 1) / (32 / NREP);
+  hipLaunchKernelGGL((paged_attn_grouped_quant_d128<NREP>), dim3(static_cast<unsigned>(groups)), dim3(512), 0, st,
+                     a, qout, ldq, qs);
+  return hipGetLastError();
+}
+
+// Checks shared by both entry points; fills `a` (output fields left unset).
+static int attn_args(AttnArgs& a, const void* q, int64_t sqt, int64_t sqh, const void* k_cache, int64_t skp,
+                     int64_t skh, const void* v_cache, int64_t svp, int64_t svh, int64_t num_slots,
+                     const int32_t* kv_indices, const int32_t* kv_start, const int32_t* kv_len, int64_t T,
+                     int64_t Hq, int64_t Hk, int64_t D, float scale, const int32_t* group_prefix) {
   if (T < 0 || Hq <= 0 || Hk <= 0 || D <= 0) return FR_EINVAL;
-  if (T == 0) return FR_OK;
-  if (!q || !k_cache || !v_cache || !kv_indices || !kv_start || !kv_len || !out) return FR_EINVAL;
+  if (T > 0 && (!q || !k_cache || !v_cache || !kv_indices || !kv_start || !kv_len)) return FR_EINVAL;
   if (D != 128 || Hq % Hk != 0) return FR_EUNSUPPORTED;
+  const int64_t nrep = Hq / Hk;
+  if (nrep != 1 && nrep != 2 && nrep != 4 && nrep != 8) return FR_EUNSUPPORTED;
   auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
   // 16-byte vector access: row and head strides in whole 16-byte units
-  if (!al16(q) || !al16(k_cache) || !al16(v_cache) || !al16(out) || sqt % 8 || sqh % 8 || sot % 8 ||
-      soh % 8 || skp % 16 || skh % 16 || svp % 16 || svh % 16)
+  if (!al16(q) || !al16(k_cache) || !al16(v_cache) || sqt % 8 || sqh % 8 || skp % 16 || skh % 16 || svp % 16 ||
+      svh % 16)
     return FR_EUNSUPPORTED;
-  AttnArgs a{};
+  a = AttnArgs{};
   a.q = static_cast<const uint16_t*>(q);
   a.sqt = sqt;
   a.sqh = sqh;
@@ -618,22 +710,65 @@ extern "C" int fr_paged_attention_fp8(const void* q, int64_t sqt, int64_t sqh, c
   a.kv_indices = kv_indices;
   a.kv_start = kv_start;
   a.kv_len = kv_len;
-  a.out = static_cast<uint16_t*>(out);
-  a.sot = sot;
-  a.soh = soh;
   a.T = T;
   a.Hq = Hq;
   a.Hk = Hk;
   a.num_slots = num_slots;
   a.qscale = scale * 1.4426950408889634f;
   a.gp = group_prefix;
+  return FR_OK;
+}
+
+extern "C" int fr_paged_attention_fp8(const void* q, int64_t sqt, int64_t sqh, const void* k_cache,
+                                      int64_t skp, int64_t skh, const void* v_cache, int64_t svp,
+                                      int64_t svh, int64_t num_slots, const int32_t* kv_indices,
+                                      const int32_t* kv_start, const int32_t* kv_len, void* out,
+                                      int64_t sot, int64_t soh, int64_t T, int64_t Hq, int64_t Hk,
+                                      int64_t D, float scale, const int32_t* group_prefix,
+                                      void* stream) {
+  AttnArgs a;
+  const int rc = attn_args(a, q, sqt, sqh, k_cache, skp, skh, v_cache, svp, svh, num_slots, kv_indices, kv_start,
+                           kv_len, T, Hq, Hk, D, scale, group_prefix);
+  if (rc != FR_OK) return rc;
+  if (T == 0) return FR_OK;
+  if (!out) return FR_EINVAL;
+  if ((reinterpret_cast<uintptr_t>(out) & 15u) || sot % 8 || soh % 8) return FR_EUNSUPPORTED;
+  a.out = static_cast<uint16_t*>(out);
+  a.sot = sot;
+  a.soh = soh;
   hipError_t e;
   switch (Hq / Hk) {
     case 1: e = launch_grouped<1>(a, static_cast<hipStream_t>(stream)); break;
     case 2: e = launch_grouped<2>(a, static_cast<hipStream_t>(stream)); break;
     case 4: e = launch_grouped<4>(a, static_cast<hipStream_t>(stream)); break;
-    case 8: e = launch_grouped<8>(a, static_cast<hipStream_t>(stream)); break;
-    default: return FR_EUNSUPPORTED;
+    default: e = launch_grouped<8>(a, static_cast<hipStream_t>(stream)); break;
+  }
+  return e == hipSuccess ? FR_OK : FR_ELAUNCH;
+}
+
+extern "C" int fr_paged_attention_quant_fp8(const void* q, int64_t sqt, int64_t sqh, const void* k_cache,
+                                            int64_t skp, int64_t skh, const void* v_cache, int64_t svp,
+                                            int64_t svh, int64_t num_slots, const int32_t* kv_indices,
+                                            const int32_t* kv_start, const int32_t* kv_len, void* out_q,
+                                            int64_t ldq, float* out_scale, int64_t T, int64_t Hq, int64_t Hk,
+                                            int64_t D, float scale, const int32_t* group_prefix, void* stream) {
+  AttnArgs a;
+  const int rc = attn_args(a, q, sqt, sqh, k_cache, skp, skh, v_cache, svp, svh, num_slots, kv_indices, kv_start,
+                           kv_len, T, Hq, Hk, D, scale, group_prefix);
+  if (rc != FR_OK) return rc;
+  // one wave per kv head in a workgroup of 8; 8-wide query groups take the
+  // token path in a kernel of their own, which this fusion does not cover
+  if (Hk > 8 || Hq / Hk == 8) return FR_EUNSUPPORTED;
+  if (T == 0) return FR_OK;
+  if (!out_q || !out_scale || ldq < Hq * D) return FR_EINVAL;
+  if ((reinterpret_cast<uintptr_t>(out_q) & 7u) || ldq % 8) return FR_EUNSUPPORTED;  // 8-byte code stores
+  uint8_t* qo = static_cast<uint8_t*>(out_q);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  switch (Hq / Hk) {
+    case 1: e = launch_grouped_quant<1>(a, qo, ldq, out_scale, st); break;
+    case 2: e = launch_grouped_quant<2>(a, qo, ldq, out_scale, st); break;
+    default: e = launch_grouped_quant<4>(a, qo, ldq, out_scale, st); break;
   }
   return e == hipSuccess ? FR_OK : FR_ELAUNCH;
 }

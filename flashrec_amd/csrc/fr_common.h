@@ -216,4 +216,51 @@ __device__ __forceinline__ float row16_sum(float v) {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+// ---------------------------------------------------------------- per-token quant
+// NaN-propagating max (v_maximum3_f32): torch's amax propagates NaN.
+__device__ __forceinline__ float maxnan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+__device__ __forceinline__ float wave_maxnan(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = maxnan(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Max of a 32-bit word's two bf16 magnitudes (and m), as bf16 bits.  For
+// |bf16| bit patterns the unsigned order is the float order with NaN above
+// inf above every finite value, so the max propagates NaN as torch's amax.
+__device__ __forceinline__ uint32_t absmax_bits(uint32_t m, uint32_t w) {
+  return __builtin_elementwise_max(m, __builtin_elementwise_max(w & 0x7FFFu, (w >> 16) & 0x7FFFu));
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1)
+    v = __builtin_elementwise_max(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), o, 64)));
+  return v;
+}
+
+// e4m3 codes of 8 values of a row whose scale is amax / 448 (r = 1 / scale),
+// torch's `(x / scale).clamp(-448, 448).to(e4m3)` (sglops.py:92-96).  A
+// finite row (amax < 3e38) has |x / scale| <= 448 within rounding, where the
+// hardware conversion equals clamp + convert, and the quotient is correctly
+// rounded (div_rn_shared); a row holding NaN or inf takes the plain IEEE
+// division and torch's NaN codes.
+__device__ __forceinline__ u32x2 quant8_e4m3(const float* v, float scale, float r, bool finite) {
+  float t[8];
+  u32x2 o;
+  if (finite) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) t[i] = div_rn_shared(v[i], scale, r);
+    o[0] = cvt_pk_e4m3<true>(t[2], t[3], cvt_pk_e4m3<false>(t[0], t[1], 0u));
+    o[1] = cvt_pk_e4m3<true>(t[6], t[7], cvt_pk_e4m3<false>(t[4], t[5], 0u));
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) t[i] = v[i] / scale;
+    o[0] = e4m3x4_clamped(t[0], t[1], t[2], t[3]);
+    o[1] = e4m3x4_clamped(t[4], t[5], t[6], t[7]);
+  }
+  return o;
+}
+
 }  // namespace fr

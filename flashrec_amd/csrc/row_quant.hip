@@ -62,15 +62,6 @@ __device__ __forceinline__ void round_bf16x2(float& a, float& b) {
   b = __uint_as_float(w & 0xFFFF0000u);
 }
 
-// NaN-propagating max (v_maximum3_f32): torch's amax propagates NaN.
-__device__ __forceinline__ float maxnan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
-
-__device__ __forceinline__ float wave_maxnan(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = maxnan(v, __shfl_xor(v, o, 64));
-  return v;
-}
-
 // silu(g) = g / (1 + exp(-g)) for |g| <= 80 (the result is rounded to bf16
 // next).  exp(-g) = 2^a with a = fl(-g * log2(e)); the quotient by
 // d = 1 + 2^a is corrected as in div_rn_shared.  The one inexact step left is
@@ -168,20 +159,6 @@ __global__ __launch_bounds__(256) void row_kernel_generic(RowArgs a) {
   generic_row<MODE, DT, QOUT>(a, row, threadIdx.x & 63);
 }
 
-// Max of a 32-bit word's two bf16 magnitudes (and m), as bf16 bits.  For
-// |bf16| bit patterns the unsigned order is the float order with NaN above
-// inf above every finite value, so the max propagates NaN as torch's amax.
-__device__ __forceinline__ uint32_t absmax_bits(uint32_t m, uint32_t w) {
-  return __builtin_elementwise_max(m, __builtin_elementwise_max(w & 0x7FFFu, (w >> 16) & 0x7FFFu));
-}
-
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1)
-    v = __builtin_elementwise_max(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), o, 64)));
-  return v;
-}
-
 template <int MODE, int NV, bool QOUT, bool FULL>
 __global__ __launch_bounds__(256) void row_kernel_vec(RowArgs a) {
   const int lane = threadIdx.x & 63;
@@ -255,31 +232,14 @@ __global__ __launch_bounds__(256) void row_kernel_vec(RowArgs a) {
     const float scale = amax / kFp8Max;
     if (lane == 0) a.s[row] = scale;
     uint8_t* qrow = a.q + row * a.ldq;
-    if (amax < 3.0e38f) {
-      const float r = 1.0f / scale;
+    const bool finite = amax < 3.0e38f;
+    const float r = 1.0f / scale;
 #pragma unroll
-      for (int j = 0; j < NV; ++j) {
-        float v[8], t[8];
-        unpack8(p[j], v);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) t[i] = div_rn_shared(v[i], scale, r);
-        u32x2 o;
-        o[0] = cvt_pk_e4m3<true>(t[2], t[3], cvt_pk_e4m3<false>(t[0], t[1], 0u));
-        o[1] = cvt_pk_e4m3<true>(t[6], t[7], cvt_pk_e4m3<false>(t[4], t[5], 0u));
-        if (in(j)) stnt(reinterpret_cast<u32x2*>(qrow + col(j)), o);
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < NV; ++j) {
-        float v[8], t[8];
-        unpack8(p[j], v);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) t[i] = v[i] / scale;
-        u32x2 o;
-        o[0] = e4m3x4_clamped(t[0], t[1], t[2], t[3]);
-        o[1] = e4m3x4_clamped(t[4], t[5], t[6], t[7]);
-        if (in(j)) stnt(reinterpret_cast<u32x2*>(qrow + col(j)), o);
-      }
+    for (int j = 0; j < NV; ++j) {
+      float v[8];
+      unpack8(p[j], v);
+      const u32x2 o = quant8_e4m3(v, scale, r, finite);
+      if (in(j)) stnt(reinterpret_cast<u32x2*>(qrow + col(j)), o);
     }
   };
 
@@ -371,33 +331,12 @@ __global__ __launch_bounds__(256) void row_kernel_vec(RowArgs a) {
     if (lane == 0) a.s[row] = scale;
 
     uint8_t* qrow = a.q + row * a.ldq;
-    if (amax < 3.0e38f) {
-      // Finite row: |x / scale| <= 448 (within rounding), where the hardware
-      // conversion equals torch's clamp + convert; the quotient is correctly
-      // rounded (Markstein correction with the row's reciprocal).
-      const float r = 1.0f / scale;
+    const bool finite = amax < 3.0e38f;
+    const float r = 1.0f / scale;
 #pragma unroll
-      for (int j = 0; j < NV; ++j) {
-        float t[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) t[i] = div_rn_shared(v[j][i], scale, r);
-        u32x2 o;
-        o[0] = cvt_pk_e4m3<true>(t[2], t[3], cvt_pk_e4m3<false>(t[0], t[1], 0u));
-        o[1] = cvt_pk_e4m3<true>(t[6], t[7], cvt_pk_e4m3<false>(t[4], t[5], 0u));
-        if (in(j)) stnt(reinterpret_cast<u32x2*>(qrow + col(j)), o);
-      }
-    } else {
-      // NaN or inf in the row: plain IEEE division and torch's NaN codes.
-#pragma unroll
-      for (int j = 0; j < NV; ++j) {
-        float t[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) t[i] = v[j][i] / scale;
-        u32x2 o;
-        o[0] = e4m3x4_clamped(t[0], t[1], t[2], t[3]);
-        o[1] = e4m3x4_clamped(t[4], t[5], t[6], t[7]);
-        if (in(j)) stnt(reinterpret_cast<u32x2*>(qrow + col(j)), o);
-      }
+    for (int j = 0; j < NV; ++j) {
+      const u32x2 o = quant8_e4m3(v[j], scale, r, finite);
+      if (in(j)) stnt(reinterpret_cast<u32x2*>(qrow + col(j)), o);
     }
   }
 }

@@ -230,9 +230,15 @@ class Qwen3FP8DecodeStep:
             raise RuntimeError("fused QK-norm/RoPE/KV write rejected its inputs")
         self._tap(L, "rope", q)
         # q stays a strided view of qkv: the attention kernel takes row and head strides
-        o = self.attn.forward(q, k, v, L.layer_id, self.batch, skip_store=True)
-        self._tap(L, "attn", o)
-        out = L.o_proj(o.reshape(t, -1))
+        if self.probe is None:
+            # attention fused with the o projection's per-token e4m3 quant
+            # (bit-for-bit the two steps below, which a probe needs apart)
+            a8, a_scale = self.attn.forward_quant_fp8(q, L.layer_id)
+            out = L.o_proj.forward_fp8(a8, a_scale, (t, s.q_heads * s.head_dim), torch.bfloat16)
+        else:
+            o = self.attn.forward(q, k, v, L.layer_id, self.batch, skip_store=True)
+            self._tap(L, "attn", o)
+            out = L.o_proj(o.reshape(t, -1))
         self._tap(L, "o", out)
         return out
 

@@ -171,6 +171,22 @@ int fr_paged_attention_fp8(const void* q, int64_t sqt, int64_t sqh, const void* 
                            int64_t Hq, int64_t Hk, int64_t D, float scale,
                            const int32_t* group_prefix, void* stream);
 
+/* fr_paged_attention_fp8 fused with the per-token e4m3 quant of its output,
+ * the input of the o projection: out_q [T, Hq * 128] e4m3 (row stride ldq
+ * bytes, a multiple of 8), out_scale [T] fp32, bit-for-bit the codes and
+ * scales of fr_paged_attention_fp8 followed by fr_per_token_quant_fp8 on its
+ * bf16 output (no bf16 output is written).  Takes Hk <= 8 and Hq / Hk in
+ * {1, 2, 4}; FR_EUNSUPPORTED otherwise (the caller then runs the two steps).
+ * Replaces the reference's attention output -> o_proj input pair,
+ * python/flashrec/models/qwen3.py:131-134 -> layers/linear.py:118-151 ->
+ * kernel/sglops.py:84-96 (per_token_quant_fp8). */
+int fr_paged_attention_quant_fp8(const void* q, int64_t sqt, int64_t sqh, const void* k_cache,
+                                 int64_t skp, int64_t skh, const void* v_cache, int64_t svp, int64_t svh,
+                                 int64_t num_slots, const int32_t* kv_indices, const int32_t* kv_start,
+                                 const int32_t* kv_len, void* out_q, int64_t ldq, float* out_scale, int64_t T,
+                                 int64_t Hq, int64_t Hk, int64_t D, float scale,
+                                 const int32_t* group_prefix, void* stream);
+
 /* The per-batch attention plan, computed once for all layers that attend
  * over the same kv_indices / kv_start / kv_len: for each group of 32 / (Hq /
  * Hk) consecutive query tokens, the slot prefix all of them share, rounded

@@ -21,9 +21,6 @@ pytestmark = pytest.mark.gpu
 CHECKED_LAYERS = (0, 27)
 
 
-CHECKED_LAYERS = (0, 27)
-
-
 @pytest.fixture(scope="module")
 def step(dev):
     from flashrec_amd.decode_step import Qwen3FP8DecodeStep, Qwen3Shape
