@@ -171,6 +171,37 @@ def _decode_step_case(dev):
     return out
 
 
+def _mfma_ceiling(dev, iters=40000):
+    """Sustained rate of the GEMM's fp8 MFMA with register operands and no
+    memory traffic (fr_calib_mfma_ceiling), one wave per SIMD on every CU,
+    with constant and with random e4m3 operands, and the shader clock the
+    kernel ran at (s_memtime over s_memrealtime): what the matrix cores reach
+    on this board under its power management."""
+    from flashrec_amd._lib import call
+
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    clocks = torch.zeros(2 * cus, dtype=torch.int64, device=dev)
+    sink = torch.zeros(256, dtype=torch.float32, device=dev)
+    st = torch.cuda.current_stream(dev).cuda_stream
+    out = {}
+    for name, rnd in (("constant_operands", 0), ("random_operands", 1)):
+        call("fr_calib_mfma_ceiling", cus, 200, rnd, clocks.data_ptr(), sink.data_ptr(), st)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        call("fr_calib_mfma_ceiling", cus, iters, rnd, clocks.data_ptr(), sink.data_ptr(), st)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1)
+        c = clocks.view(cus, 2).double().cpu()
+        ghz = float((c[:, 0] / c[:, 1]).mean()) * 0.1
+        flops = cus * 4 * iters * 4 * 2.0 * 32 * 32 * 64
+        out[name] = {"TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1), "sclk_GHz": round(ghz, 3),
+                     "frac_of_5PF": round(flops / (ms * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4)}
+    out["what"] = ("v_mfma_scale_f32_32x32x64_f8f6f4 on register operands, 4 chains per wave, one wave per "
+                   "SIMD, no memory traffic; mean over the launch (HIP events)")
+    return out
+
+
 def _bw_case(fn_factory, dev, nbytes, reps):
     step, cleanup = fn_factory()
     ms = _graph_timed(step, reps)
@@ -390,7 +421,15 @@ def main() -> int:
     ap.add_argument("--quick", action="store_true", help="headline GEMM only")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 20 copies of a 256 MiB buffer (rocprof FETCH/WRITE_SIZE scale)")
+    ap.add_argument("--mfma-ceiling", action="store_true",
+                    help="only measure the fp8 MFMA rate on register operands (constant and random)")
     args = ap.parse_args()
+    if args.mfma_ceiling:
+        from flashrec_amd._lib import load
+
+        load()
+        print(json.dumps(_mfma_ceiling(torch.device("cuda:0"))))
+        return 0
     if args.copy_calibration:
         src = torch.empty(256 * 2**20, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
@@ -439,6 +478,7 @@ def main() -> int:
     extra = {}
     if not args.quick:
         steps, warm = max(20, args.steps), args.warmup
+        extra["mfma_ceiling"] = _mfma_ceiling(dev)
         ms1, tf1 = _gemm_case(dev, 512, 12288, 2048, steps, warm, seed=11)
         extra["config1_gemm_M512"] = {"ms": round(ms1, 5), "TFLOP/s": round(tf1, 2),
                                       "frac": round(tf1 / PEAK_FP8_TFLOPS, 4)}

@@ -94,6 +94,7 @@ SIGNATURES = {
         _P, _I64, _P, _I64, _I64, _I64, _I64, _F32, _P, _P,  # codes, ldq, scales, T, Hq, Hk, D, scale, plan, stream
     ],
     "fr_paged_attention_plan_size": [_I64, _I64, _I64],
+    "fr_calib_mfma_ceiling": [_I64, _I64, _I32, _P, _P, _P],
     "fr_paged_attention_plan": [_P, _P, _P, _I64, _I64, _I64, _P, _P],
 }
 

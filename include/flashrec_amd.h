@@ -302,6 +302,16 @@ int fr_row_topk(const float* x, int64_t ldx, int64_t R, int64_t V, int64_t C,
 int fr_log_softmax_f32(const float* x, int64_t ldx, float* out, int64_t ldo, int64_t M,
                        int64_t N, void* stream);
 
+/* Measurement only, no counterpart in the reference: `blocks` workgroups of
+ * four waves each run `iters` rounds of four v_mfma_scale_f32_32x32x64_f8f6f4
+ * (2 * 32 * 32 * 64 flops each) on register operands, random e4m3 bytes when
+ * random_operands is nonzero, else one constant byte; clocks[2 * b] and
+ * clocks[2 * b + 1] receive workgroup b's s_memtime and s_memrealtime
+ * (100 MHz) spans of the loop.  sink ([256] fp32) is never written in
+ * practice.  bench.py --mfma-ceiling reports the sustained rate and clock. */
+int fr_calib_mfma_ceiling(int64_t blocks, int64_t iters, int random_operands, uint64_t* clocks, float* sink,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif
