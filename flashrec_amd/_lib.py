@@ -46,6 +46,8 @@ SIGNATURES = {
     "fr_silu_quant_fp8": [_P, _I32, _I64, _I64, _I64, _P, _P, _P],
     "fr_silu_and_mul": [_P, _I32, _I64, _P, _I64, _I64, _I64, _P],
     "fr_fp8_scaled_mm": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I32, _P],
+    "fr_fp8_scaled_mm_residual": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64,
+                                  _I32, _P],
     "fr_qk_norm_rope_store_fp8": [
         _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,  # q, k, v + strides
         _P, _P, _P, _P, _F32, _P, _I64,  # pos, loc, qw, kw, eps, cos_sin, rows

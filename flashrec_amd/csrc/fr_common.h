@@ -68,9 +68,20 @@ __device__ __forceinline__ float fp16_to_f32(uint16_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }
 
+// fp32 -> fp16, round to nearest even, of a value already rounded to fp32.
+// The empty asm pins the fp32 value: without it the compiler may fold the
+// multiply that produced it into the conversion (v_fma_mixlo_f16 with a zero
+// addend: one rounding of the exact product), while torch rounds the fp32
+// product and then converts it; the two differ where the fp32 rounding
+// lands on an fp16 halfway point.
+__device__ __forceinline__ _Float16 to_fp16(float x) {
+  asm("" : "+v"(x));
+  return static_cast<_Float16>(x);
+}
+
 __device__ __forceinline__ uint32_t pack_fp16x2(float lo, float hi) {
-  _Float16 a = static_cast<_Float16>(lo);
-  _Float16 b = static_cast<_Float16>(hi);
+  _Float16 a = to_fp16(lo);
+  _Float16 b = to_fp16(hi);
   return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
          (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
 }
@@ -93,12 +104,8 @@ template <>
 struct Elem<FR_DTYPE_FP16> {
   using T = uint16_t;
   static __device__ __forceinline__ float load(const T* p) { return fp16_to_f32(*p); }
-  static __device__ __forceinline__ float round(float x) {
-    return static_cast<float>(static_cast<_Float16>(x));
-  }
-  static __device__ __forceinline__ uint16_t bits(float x) {
-    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
-  }
+  static __device__ __forceinline__ float round(float x) { return static_cast<float>(to_fp16(x)); }
+  static __device__ __forceinline__ uint16_t bits(float x) { return __builtin_bit_cast(uint16_t, to_fp16(x)); }
 };
 template <>
 struct Elem<FR_DTYPE_FP32> {

@@ -55,6 +55,10 @@ struct GemmArgs {
   void* out;
   int64_t ldo;
   int64_t M, N, K;
+  // residual rows (out dtype, 16-bit outputs only) added to the rounded
+  // product: out = rnd(rnd(product) + res); may alias out (same ldo), or null
+  const void* res;
+  int64_t ldr;
 };
 
 constexpr int kBK = 64;  // bytes of K per MFMA step
@@ -176,10 +180,11 @@ struct OutT {
   static constexpr int kBytes = OUT == FR_DTYPE_FP32 ? 4 : 2;
 };
 
-// Four consecutive outputs of one row, with optional bias, bounds-checked.
+// Four consecutive outputs of one row, with optional bias and residual,
+// bounds-checked.
 template <int OUT>
 __device__ __forceinline__ void store4(void* out, int64_t ldo, int64_t m, int64_t n, int64_t N,
-                                       const float* v, const void* bias) {
+                                       const float* v, const void* bias, const void* res, int64_t ldr) {
   float t[4] = {v[0], v[1], v[2], v[3]};
   if (OUT == FR_DTYPE_FP32) {
     float* o = static_cast<float*>(out) + m * ldo + n;
@@ -197,6 +202,15 @@ __device__ __forceinline__ void store4(void* out, int64_t ldo, int64_t m, int64_
     const uint16_t* bb = static_cast<const uint16_t*>(bias) + n;
     for (int i = 0; i < 4; ++i)
       if (n + i < N) t[i] += (OUT == FR_DTYPE_BF16) ? bf16_to_f32(bb[i]) : fp16_to_f32(bb[i]);
+  }
+  if (res) {
+    // the product is stored in the output dtype first, then added
+    const uint16_t* rr = static_cast<const uint16_t*>(res) + m * ldr + n;
+    for (int i = 0; i < 4; ++i)
+      if (n + i < N)
+        t[i] = OUT == FR_DTYPE_BF16 ? round_bf16(t[i]) + bf16_to_f32(rr[i])
+                                    : fp16_to_f32(static_cast<uint16_t>(pack_fp16x2(t[i], 0.0f) & 0xFFFFu)) +
+                                          fp16_to_f32(rr[i]);
   }
   uint32_t lo = OUT == FR_DTYPE_BF16 ? pack_bf16x2(t[0], t[1]) : pack_fp16x2(t[0], t[1]);
   uint32_t hi = OUT == FR_DTYPE_BF16 ? pack_bf16x2(t[2], t[3]) : pack_fp16x2(t[2], t[3]);
@@ -422,7 +436,14 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     tile_coords(blockIdx.x + local * G, nt, tilesM, tm, tn);
     const int64_t m0 = tm * BM + wm * WM;
     const int64_t n0 = tn * BN + wn * WN;
+    // the residual add is compiled into the fast path of the tiles that have
+    // registers to spare for it (not the 256 x 256 tile); others take the
+    // bounds-checked path for it
+    constexpr bool kResFast = !(BN == 256 && BM == 256);
     const bool fast = tm * BM + BM <= g.M && tn * BN + BN <= g.N && g.bias == nullptr &&
+                      (g.res == nullptr ||
+                       (kResFast && (g.ldr * EB) % 16 == 0 && (reinterpret_cast<uintptr_t>(g.res) & 15) == 0 &&
+                        g.ldr < (int64_t(1) << 22))) &&
                       (g.ldo * EB) % 16 == 0 && (reinterpret_cast<uintptr_t>(g.out) & 15) == 0 &&
                       g.ldo < (int64_t(1) << 22);  // tile offsets fit the 32-bit store offsets
     if (!fast) {
@@ -444,7 +465,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
               const int64_t nn = n + t < g.N ? n + t : g.N - 1;
               v[t] = (acc[i][j][4 * q + t] * sam) * g.sb[nn * g.sb_stride];
             }
-            store4<OUT>(g.out, g.ldo, m, n, g.N, v, g.bias);
+            store4<OUT>(g.out, g.ldo, m, n, g.N, v, g.bias, g.res, g.ldr);
           }
       }
       // Retire this path's scale and bias loads here: the compiler's wait
@@ -544,6 +565,46 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
       }
     };
     u32x4 w[NR];
+    // residual rows (16-bit outputs): read with the same segment layout as
+    // the stores, one pass ahead, and added to the converted product
+    const bool has_res = kResFast && EB == 2 && g.res != nullptr;
+    const uint64_t rbase =
+        has_res ? reinterpret_cast<uint64_t>(static_cast<const uint8_t*>(g.res) + (m0 * g.ldr + n0) * EB) : 0;
+    // (readfirstlane returns int: each word goes through uint32_t before it
+    // is widened, or a low word with bit 31 set would sign-extend into the
+    // high word)
+    const uint32_t rlo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(rbase));
+    const uint32_t rhi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(rbase >> 32));
+    const __amdgpu_buffer_rsrc_t rres =
+        make_rsrc(reinterpret_cast<const void*>((static_cast<uint64_t>(rhi) << 32) | rlo), 0xFFFFFFFFu);
+    const uint32_t ldr32 = static_cast<uint32_t>(g.ldr);
+    const uint32_t vr = ((lx / CPRS) * ldr32 + (lx % CPRS) * (16 / EB)) * EB;
+    u32x4 rv[2][NR];
+    auto load_res = [&](int t) __attribute__((always_inline)) {
+      const int cg = t / FM, j = t % FM;
+#pragma unroll
+      for (int rr = 0; rr < NR; ++rr)
+        rv[t & 1][rr] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       rres, vr, static_cast<int>(((j * 32 + rr * RPR) * ldr32 + cg * CPP) * EB), 0));
+    };
+    auto add_res = [&](int t) __attribute__((always_inline)) {
+#pragma unroll
+      for (int rr = 0; rr < NR; ++rr)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t pw = w[rr][e], rw = rv[t & 1][rr][e];
+          if constexpr (OUT == FR_DTYPE_BF16) {
+            w[rr][e] = pack_bf16x2(__uint_as_float(pw << 16) + __uint_as_float(rw << 16),
+                                   __uint_as_float(pw & 0xFFFF0000u) + __uint_as_float(rw & 0xFFFF0000u));
+          } else {
+            w[rr][e] = pack_fp16x2(fp16_to_f32(static_cast<uint16_t>(pw & 0xFFFFu)) +
+                                       fp16_to_f32(static_cast<uint16_t>(rw & 0xFFFFu)),
+                                   fp16_to_f32(static_cast<uint16_t>(pw >> 16)) +
+                                       fp16_to_f32(static_cast<uint16_t>(rw >> 16)));
+          }
+        }
+    };
     auto read_back = [&]() __attribute__((always_inline)) {
 #pragma unroll
       for (int rr = 0; rr < NR; ++rr) w[rr] = lds_read_b128_nw(ra[rr]);
@@ -573,11 +634,13 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
       else
         static_assert(NR == 0, "pass shape");
     };
+    if (has_res) load_res(0);
     compute(0);
     stage();
     read_back();
 #pragma unroll
     for (int t = 0; t < NP; ++t) {
+      if (has_res && t + 1 < NP) load_res(t + 1);
       if (t + 1 < NP && (t + 1) % FM == 0) {
         // next column group: its scales replace this group's (already applied)
         load_sb((t + 1) / FM);
@@ -585,6 +648,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
       }
       if (t + 1 < NP) compute(t + 1);
       wait_reads();
+      if (has_res) add_res(t);
       const int cg = t / FM, j = t % FM;
 #pragma unroll
       for (int rr = 0; rr < NR; ++rr)
@@ -776,7 +840,7 @@ __global__ __launch_bounds__(256) void gemm_fp8_scalar(GemmArgs g) {
     acc += __builtin_amdgcn_cvt_f32_fp8(ar[k], 0) * __builtin_amdgcn_cvt_f32_fp8(br[k], 0);
   float v[4] = {(acc * g.sa[m * g.sa_stride]) * g.sb[n * g.sb_stride], 0.f, 0.f, 0.f};
   // store one element through the 4-wide helper with N clipped to n + 1
-  store4<OUT>(g.out, g.ldo, m, n, n + 1, v, g.bias);
+  store4<OUT>(g.out, g.ldo, m, n, n + 1, v, g.bias, g.res, g.ldr);
 }
 
 static int num_cus() {
@@ -872,11 +936,10 @@ static hipError_t dispatch(const GemmArgs& g, hipStream_t st) {
 
 using namespace fr;
 
-extern "C" int fr_fp8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
-                                const float* scale_a, int64_t scale_a_numel,
-                                const float* scale_b, int64_t scale_b_numel, const void* bias,
-                                int64_t bias_numel, void* out, int64_t ldo, int64_t M, int64_t N, int64_t K,
-                                int out_dtype, void* stream) {
+static int gemm_entry(const void* a, int64_t lda, const void* b, int64_t ldb, const float* scale_a,
+                      int64_t scale_a_numel, const float* scale_b, int64_t scale_b_numel, const void* bias,
+                      int64_t bias_numel, const void* res, int64_t ldr, void* out, int64_t ldo, int64_t M,
+                      int64_t N, int64_t K, int out_dtype, void* stream) {
   if (M < 0 || N < 0 || K < 0) return FR_EINVAL;
   if (M == 0 || N == 0) return FR_OK;
   if (!a || !b || !scale_a || !scale_b || !out) return FR_EINVAL;
@@ -900,6 +963,8 @@ extern "C" int fr_fp8_scaled_mm(const void* a, int64_t lda, const void* b, int64
   g.M = M;
   g.N = N;
   g.K = K;
+  g.res = res;
+  g.ldr = ldr;
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t err;
   switch (out_dtype) {
@@ -909,4 +974,27 @@ extern "C" int fr_fp8_scaled_mm(const void* a, int64_t lda, const void* b, int64
     default: return FR_EINVAL;
   }
   return err == hipSuccess ? FR_OK : FR_ELAUNCH;
+}
+
+extern "C" int fr_fp8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
+                                const float* scale_a, int64_t scale_a_numel,
+                                const float* scale_b, int64_t scale_b_numel, const void* bias,
+                                int64_t bias_numel, void* out, int64_t ldo, int64_t M, int64_t N, int64_t K,
+                                int out_dtype, void* stream) {
+  return gemm_entry(a, lda, b, ldb, scale_a, scale_a_numel, scale_b, scale_b_numel, bias, bias_numel, nullptr, 0,
+                    out, ldo, M, N, K, out_dtype, stream);
+}
+
+extern "C" int fr_fp8_scaled_mm_residual(const void* a, int64_t lda, const void* b, int64_t ldb,
+                                         const float* scale_a, int64_t scale_a_numel, const float* scale_b,
+                                         int64_t scale_b_numel, const void* residual, int64_t ldr, void* out,
+                                         int64_t ldo, int64_t M, int64_t N, int64_t K, int out_dtype,
+                                         void* stream) {
+  if (out_dtype != FR_DTYPE_BF16 && out_dtype != FR_DTYPE_FP16) return out_dtype == FR_DTYPE_FP32 ? FR_EUNSUPPORTED
+                                                                                                    : FR_EINVAL;
+  if (M > 0 && N > 0 && (!residual || ldr < N)) return FR_EINVAL;
+  // in place only row for row: an aliased residual must share the output's stride
+  if (residual == out && ldr != ldo) return FR_EINVAL;
+  return gemm_entry(a, lda, b, ldb, scale_a, scale_a_numel, scale_b, scale_b_numel, nullptr, 0, residual, ldr, out,
+                    ldo, M, N, K, out_dtype, stream);
 }

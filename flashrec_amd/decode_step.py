@@ -213,8 +213,10 @@ class Qwen3FP8DecodeStep:
             self._init_beam(requests, beams, trie_items, trie_levels, trie_codes, gen, step)
 
     # ------------------------------------------------------------ one layer
-    def _attention(self, L: _Layer, q_fp8, a_scale) -> torch.Tensor:
-        """qwen3.py:65-136, fused fp8 path."""
+    def _attention(self, L: _Layer, q_fp8, a_scale, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """qwen3.py:65-136, fused fp8 path.  With ``residual`` the o projection
+        adds its output into the residual stream in its epilogue (the add of
+        the next fused add + RMSNorm) and returns the updated stream."""
         s = self.shape
         t = int(q_fp8.shape[0])
         qkv = L.qkv_proj.forward_fp8(q_fp8, a_scale, (t, s.hidden), torch.bfloat16)
@@ -234,6 +236,8 @@ class Qwen3FP8DecodeStep:
             # attention fused with the o projection's per-token e4m3 quant
             # (bit-for-bit the two steps below, which a probe needs apart)
             a8, a_scale = self.attn.forward_quant_fp8(q, L.layer_id)
+            if residual is not None:
+                return L.o_proj.forward_fp8_residual(a8, a_scale, residual)
             out = L.o_proj.forward_fp8(a8, a_scale, (t, s.q_heads * s.head_dim), torch.bfloat16)
         else:
             o = self.attn.forward(q, k, v, L.layer_id, self.batch, skip_store=True)
@@ -248,6 +252,8 @@ class Qwen3FP8DecodeStep:
 
     def _layer(self, L: _Layer, x: torch.Tensor, residual: Optional[torch.Tensor]):
         """qwen3.py:197-210 (fused RMSNorm->fp8 path) and the MLP of :146-171."""
+        if self.probe is None:
+            return self._layer_folded(L, x, residual)
         if residual is None:
             residual = x
             q_fp8, a_scale = L.input_layernorm.quant_fp8(x)
@@ -266,6 +272,24 @@ class Qwen3FP8DecodeStep:
         self._tap(L, "down", hidden)
         return hidden, residual
 
+    def _layer_folded(self, L: _Layer, x: Optional[torch.Tensor], residual: Optional[torch.Tensor]):
+        """The same layer with each residual add folded into the GEMM that
+        produces the addend (o_proj, down_proj: fr_fp8_scaled_mm_residual),
+        so both RMSNorms run without their add: bit-for-bit ``_layer``, whose
+        fused add + RMSNorm rounds the GEMM output and then the sum the same
+        way.  Takes and returns (None, residual) once the stream holds the
+        sum; the first layer starts from (x, None) as ``_layer`` does."""
+        if residual is None:
+            residual = x
+        q_fp8, a_scale = L.input_layernorm.quant_fp8(residual)
+        residual = self._attention(L, q_fp8, a_scale, residual)
+        q_fp8, a_scale = L.post_attention_layernorm.quant_fp8(residual)
+        t = int(q_fp8.shape[0])
+        gu = L.gate_up_proj.forward_fp8(q_fp8, a_scale, (t, self.shape.hidden), torch.bfloat16)
+        y_fp8, y_scale = silu_and_mul_per_token_quant_fp8(gu)
+        residual = L.down_proj.forward_fp8_residual(y_fp8, y_scale, residual)
+        return None, residual
+
     def forward(self, x: Optional[torch.Tensor] = None, layers: Optional[int] = None) -> torch.Tensor:
         """Decoder layers, final norm, SID-restricted fp8 lm_head -> logprobs [rows, sid_tokens]."""
         x = self.hidden_in if x is None else x
@@ -275,7 +299,10 @@ class Qwen3FP8DecodeStep:
         x = x.clone()
         for L in self.layers[: layers if layers is not None else len(self.layers)]:
             x, residual = self._layer(L, x, residual)
-        y, _ = self.final_norm(x, residual)
+        if x is None:  # folded layers: the stream already holds the last sum
+            y = self.final_norm(residual)
+        else:
+            y, _ = self.final_norm(x, residual)
         logprobs, _ = self.lm_head.compute(y, self.embed)
         return logprobs
 

@@ -175,6 +175,56 @@ def fp8_scaled_mm(
 
 
 @torch.compiler.disable
+def fp8_scaled_mm_residual(
+    a_fp8: torch.Tensor,
+    b_fp8: torch.Tensor,
+    scale_a: torch.Tensor,
+    scale_b: torch.Tensor,
+    residual: torch.Tensor,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """``residual + fp8_scaled_mm(a, b, scale_a, scale_b, residual.dtype)`` in
+    one kernel, both roundings as the two steps (the product to the residual's
+    dtype, then the sum; sglops.py:53-55).  ``out`` defaults to ``residual``
+    itself (updated in place, as fused_add_rmsnorm updates it); returns it.
+    residual: [M, N] bf16 or fp16 with a unit inner stride."""
+    if a_fp8.dtype != torch.float8_e4m3fn or b_fp8.dtype != torch.float8_e4m3fn:
+        raise TypeError("fp8_scaled_mm_residual takes float8_e4m3fn operands")
+    if residual.dtype not in _HALF:
+        raise TypeError(f"the residual must be bf16 or fp16, got {residual.dtype}")
+    if a_fp8.dim() != 2 or b_fp8.dim() != 2 or a_fp8.shape[1] != b_fp8.shape[0]:
+        raise ValueError(f"shape mismatch: a {tuple(a_fp8.shape)} b {tuple(b_fp8.shape)}")
+    m, k = int(a_fp8.shape[0]), int(a_fp8.shape[1])
+    n = int(b_fp8.shape[1])
+    if residual.dim() != 2 or tuple(residual.shape) != (m, n) or residual.stride(1) != 1:
+        raise ValueError(f"residual must be [{m}, {n}] with a unit inner stride, got {tuple(residual.shape)}")
+    if out is None:
+        out = residual
+    if out.dtype != residual.dtype or tuple(out.shape) != (m, n) or out.stride(1) != 1:
+        raise ValueError("out must match the residual's dtype and shape with a unit inner stride")
+    if out.data_ptr() == residual.data_ptr() and out.stride(0) != residual.stride(0):
+        raise ValueError("an aliased out must share the residual's row stride")
+    require_device(a_fp8, b_fp8, residual, out)
+    a = a_fp8 if a_fp8.stride(1) == 1 and (m <= 1 or a_fp8.stride(0) >= k) else a_fp8.contiguous()
+    b = b_fp8
+    if not (b.stride(0) == 1 and (n <= 1 or b.stride(1) >= k)):
+        b = b.t().contiguous().t()
+    a, b, k = _mfma_operands(a, b, m, n, k)
+    sa = scale_a.reshape(-1).to(device=a.device, dtype=torch.float32).contiguous()
+    sb = scale_b.reshape(-1).to(device=a.device, dtype=torch.float32).contiguous()
+    if sa.numel() not in (1, m) or sb.numel() not in (1, n):
+        raise ValueError("scale_a must have 1 or M values and scale_b 1 or N values")
+    lda = a.stride(0) if m > 1 else k
+    ldb = b.stride(1) if n > 1 else k
+    ldr = residual.stride(0) if m > 1 else n
+    ldo = out.stride(0) if m > 1 else n
+    call("fr_fp8_scaled_mm_residual", a.data_ptr(), lda, b.data_ptr(), ldb, sa.data_ptr(), sa.numel(),
+         sb.data_ptr(), sb.numel(), residual.data_ptr(), ldr, out.data_ptr(), ldo, m, n, k,
+         DTYPE_CODE[residual.dtype], stream_of(a))
+    return out
+
+
+@torch.compiler.disable
 def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
     """SwiGLU: ``silu(x[..., :d]) * x[..., d:]`` with ``d = last_dim // 2`` (sglops.py:143-151)."""
     require_device(x)

@@ -34,7 +34,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from flashrec_amd._lib import DTYPE_CODE, call, require_device, stream_of
-from flashrec_amd.kernel.sglops import fp8_scaled_mm, per_token_quant_fp8
+from flashrec_amd.kernel.sglops import fp8_scaled_mm, fp8_scaled_mm_residual, per_token_quant_fp8
 
 _E4M3 = torch.float8_e4m3fn
 _FP8_DTYPES = frozenset({torch.float8_e4m3fn, torch.float8_e5m2})
@@ -181,3 +181,18 @@ class Linear(nn.Module):
         bias = None if self.bias is None else self.bias.to(dtype=out_dtype)
         out = fp8_scaled_mm(q, self.w_codes.t(), a_scale, self.w_scale, out_dtype, bias)
         return out.view(*tuple(orig_shape)[:-1], self.out_features)
+
+    def forward_fp8_residual(self, q: torch.Tensor, a_scale: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
+        """``residual += forward_fp8(q, a_scale, ...)`` with the add in the GEMM's
+        epilogue (the product rounded to the residual's dtype, then the sum,
+        as a separate add would round them); ``residual`` ``[M, out_features]``
+        is updated in place and returned.  No bias (the layers this serves
+        have none)."""
+        if self.w_codes is None:
+            raise RuntimeError("Linear.forward_fp8_residual needs fp8 weights")
+        if self.bias is not None:
+            raise ValueError("forward_fp8_residual takes a Linear without bias")
+        if self.w_codes.device != q.device:
+            raise ValueError(f"activations on {q.device}, fp8 weights on {self.w_codes.device}: "
+                             "move the module with .to() first")
+        return fp8_scaled_mm_residual(q, self.w_codes.t(), a_scale, self.w_scale, residual)

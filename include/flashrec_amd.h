@@ -93,6 +93,22 @@ int fr_fp8_scaled_mm(const void* a, int64_t lda, const void* b, int64_t ldb,
                      int64_t scale_b_numel, const void* bias, int64_t bias_numel, void* out,
                      int64_t ldo, int64_t M, int64_t N, int64_t K, int out_dtype, void* stream);
 
+/* fr_fp8_scaled_mm with the residual add of the next RMSNorm folded into
+ * its epilogue: out[m, n] = rnd(rnd(product[m, n]) + residual[m, n]) for
+ * 16-bit out_dtype (bf16 or fp16; fp32 gives FR_EUNSUPPORTED), rnd the
+ * rounding to out_dtype; residual [M, N] of out_dtype with row stride ldr.
+ * out may be residual itself (then ldr must equal ldo): the residual
+ * stream updated in place.  No bias.  Bit-for-bit fr_fp8_scaled_mm followed
+ * by the residual update of fused_add_rmsnorm (python/flashrec/kernel/
+ * sglops.py:53-55, residual = residual + x in the activation dtype), so the
+ * RMSNorm that follows runs without its add.  Replaces, in the decoder layer
+ * (python/flashrec/models/qwen3.py:197-210), o_proj / down_proj followed by
+ * the add half of the next fused add + RMSNorm. */
+int fr_fp8_scaled_mm_residual(const void* a, int64_t lda, const void* b, int64_t ldb, const float* scale_a,
+                              int64_t scale_a_numel, const float* scale_b, int64_t scale_b_numel,
+                              const void* residual, int64_t ldr, void* out, int64_t ldo, int64_t M, int64_t N,
+                              int64_t K, int out_dtype, void* stream);
+
 /* Per-head RMSNorm of q and k (weights q_weight, k_weight: bf16 [D]),
  * NeoX rotate-half RoPE from cos_sin_cache ([cache_rows, D] fp32: cos for
  * i < D/2, sin after), q rotated in place (bf16), rotated k and raw v

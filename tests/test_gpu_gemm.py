@@ -275,3 +275,17 @@ def test_gemm_integer_exact_pow2_scales(dev, m, n, k, out_dtype):
     out = _run(dev, qa, sa.float(), qw, sw.float(), out_dtype=out_dtype)
     ref = ((a @ w.t()) * sa * sw[None, :]).to(out_dtype)
     assert torch.equal(out.cpu(), ref)
+
+
+@pytest.mark.parametrize("m,n,k", [(4096, 12288, 2048), (4096, 2048, 2048), (512, 12288, 2048), (300, 520, 384)])
+def test_gemm_16bit_outputs_round_the_fp32_product(dev, m, n, k):
+    """bf16 / fp16 outputs are the fp32 output rounded once more (torch's
+    ``(out.float() * sa * sb).to(dtype)``, sglops.py:111-139): bit-exact on
+    the 256x256, 256x128 and 192x128 tiles and on edge tiles.  (The compiler
+    once folded the last fp32 multiply into the fp16 conversion, one rounding
+    instead of two, which differed at fp16 halfway points.)"""
+    qa, sa, qw, sw = _operands(m, n, k, seed=m + k)
+    f32 = _run(dev, qa, sa, qw, sw, torch.float32)
+    for dt in (torch.bfloat16, torch.float16):
+        got = _run(dev, qa, sa, qw, sw, dt)
+        assert torch.equal(got.view(torch.int16).cpu(), f32.to(dt).view(torch.int16).cpu()), dt
