@@ -68,22 +68,23 @@ __device__ __forceinline__ float fp16_to_f32(uint16_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }
 
-// fp32 -> fp16, round to nearest even, of a value already rounded to fp32.
-// The empty asm pins the fp32 value: without it the compiler may fold the
-// multiply that produced it into the conversion (v_fma_mixlo_f16 with a zero
-// addend: one rounding of the exact product), while torch rounds the fp32
-// product and then converts it; the two differ where the fp32 rounding
-// lands on an fp16 halfway point.
+// fp32 -> fp16, round to nearest even, of a value already rounded to fp32,
+// as one v_cvt_f16_f32 written as asm (fp16 bits in the low half, high half
+// zero): a plain cast lets the compiler fold the multiply that produced x
+// into the conversion (v_fma_mixlo_f16 with a zero addend: one rounding of
+// the exact product), while torch rounds the fp32 product and then converts
+// it; the two differ where the fp32 rounding lands on an fp16 halfway point.
+__device__ __forceinline__ uint32_t fp16_bits(float x) {
+  uint32_t r;
+  asm("v_cvt_f16_f32 %0, %1" : "=v"(r) : "v"(x));
+  return r & 0xFFFFu;
+}
 __device__ __forceinline__ _Float16 to_fp16(float x) {
-  asm("" : "+v"(x));
-  return static_cast<_Float16>(x);
+  return __builtin_bit_cast(_Float16, static_cast<uint16_t>(fp16_bits(x)));
 }
 
 __device__ __forceinline__ uint32_t pack_fp16x2(float lo, float hi) {
-  _Float16 a = to_fp16(lo);
-  _Float16 b = to_fp16(hi);
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
-         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
+  return fp16_bits(lo) | (fp16_bits(hi) << 16);
 }
 
 // Element loader: the activation dtype is a template parameter so the row

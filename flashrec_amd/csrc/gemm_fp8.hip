@@ -132,6 +132,20 @@ __device__ __forceinline__ float lds_read_f32_nw(uint32_t a) {
   asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(a) : "memory");
   return r;
 }
+// The same reads with their wait inside the asm: the register is final when
+// the statement ends.  A read without its wait is only safe while nothing
+// touches its register before lds_wait_all; where the compiler spills in the
+// epilogue it could store such a register before the data arrived.
+__device__ __forceinline__ u32x4 lds_read_b128_wait(uint32_t a) {
+  u32x4 r;
+  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(a) : "memory");
+  return r;
+}
+__device__ __forceinline__ float lds_read_f32_wait(uint32_t a) {
+  float r;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(a) : "memory");
+  return r;
+}
 template <int NV, int NF>
 __device__ __forceinline__ void lds_wait_all(u32x4 (&v)[NV], float (&f)[NF]) {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -521,11 +535,16 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     // scales: sa of the wave's rows up front, sb per column group
     u32x4 sb4[NQ];
     float sam_r[FM];
+    // fp16 outputs: the conversion's extra registers make the compiler spill
+    // in this epilogue, and a spilled register of a read still in flight would
+    // be stored stale, so that variant waits inside each read
+    constexpr bool kSafeReads = OUT == FR_DTYPE_FP16;
     auto load_sb = [&](int cg) __attribute__((always_inline)) {
 #pragma unroll
       for (int u = 0; u < NQ; ++u) {
         if (sb_vec) {
-          sb4[u] = lds_read_b128_nw(sbl + 4 * (cg * CPP + 8 * u));
+          if constexpr (kSafeReads) sb4[u] = lds_read_b128_wait(sbl + 4 * (cg * CPP + 8 * u));
+          else sb4[u] = lds_read_b128_nw(sbl + 4 * (cg * CPP + 8 * u));
         } else {
           const uint32_t b0 = __float_as_uint(sb0);
           sb4[u] = u32x4{b0, b0, b0, b0};
@@ -533,7 +552,8 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
       }
     };
 #pragma unroll
-    for (int j = 0; j < FM; ++j) sam_r[j] = sa_vec ? lds_read_f32_nw(sal + 128 * j) : sa0;
+    for (int j = 0; j < FM; ++j)
+      sam_r[j] = sa_vec ? (kSafeReads ? lds_read_f32_wait(sal + 128 * j) : lds_read_f32_nw(sal + 128 * j)) : sa0;
     load_sb(0);
     lds_wait_all(sb4, sam_r);
     PkT pk[NQ];
@@ -607,7 +627,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     };
     auto read_back = [&]() __attribute__((always_inline)) {
 #pragma unroll
-      for (int rr = 0; rr < NR; ++rr) w[rr] = lds_read_b128_nw(ra[rr]);
+      for (int rr = 0; rr < NR; ++rr) w[rr] = kSafeReads ? lds_read_b128_wait(ra[rr]) : lds_read_b128_nw(ra[rr]);
     };
     // one wait for the reads, taking the next pass's values as operands so
     // their arithmetic stays ahead of it
