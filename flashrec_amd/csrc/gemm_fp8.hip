@@ -255,7 +255,7 @@ __device__ __forceinline__ void tile_coords(int64_t pid, int64_t nt, int64_t til
 // so each direct-to-LDS load covers whole 128-byte lines), NSL: ring depth
 // in slots, KTAIL: K % 128 != 0 (the last K steps are partly or wholly
 // zero-filled).
-template <int BN, int BM, int NSL, int RB, int OUT, bool KTAIL>
+template <int BN, int BM, int NSL, int RB, int OUT, bool KTAIL, bool RES>
 __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   // The host pass only needs the kernel's signature (for its launch stub);
   // the body uses device-only buffer-resource builtins.
@@ -455,9 +455,8 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     // bounds-checked path for it
     constexpr bool kResFast = !(BN == 256 && BM == 256);
     const bool fast = tm * BM + BM <= g.M && tn * BN + BN <= g.N && g.bias == nullptr &&
-                      (g.res == nullptr ||
-                       (kResFast && (g.ldr * EB) % 16 == 0 && (reinterpret_cast<uintptr_t>(g.res) & 15) == 0 &&
-                        g.ldr < (int64_t(1) << 22))) &&
+                      (!RES || (kResFast && (g.ldr * EB) % 16 == 0 &&
+                                (reinterpret_cast<uintptr_t>(g.res) & 15) == 0 && g.ldr < (int64_t(1) << 22))) &&
                       (g.ldo * EB) % 16 == 0 && (reinterpret_cast<uintptr_t>(g.out) & 15) == 0 &&
                       g.ldo < (int64_t(1) << 22);  // tile offsets fit the 32-bit store offsets
     if (!fast) {
@@ -479,7 +478,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
               const int64_t nn = n + t < g.N ? n + t : g.N - 1;
               v[t] = (acc[i][j][4 * q + t] * sam) * g.sb[nn * g.sb_stride];
             }
-            store4<OUT>(g.out, g.ldo, m, n, g.N, v, g.bias, g.res, g.ldr);
+            store4<OUT>(g.out, g.ldo, m, n, g.N, v, g.bias, RES ? g.res : nullptr, g.ldr);
           }
       }
       // Retire this path's scale and bias loads here: the compiler's wait
@@ -587,7 +586,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     u32x4 w[NR];
     // residual rows (16-bit outputs): read with the same segment layout as
     // the stores, one pass ahead, and added to the converted product
-    const bool has_res = kResFast && EB == 2 && g.res != nullptr;
+    constexpr bool has_res = RES && kResFast && EB == 2;
     const uint64_t rbase =
         has_res ? reinterpret_cast<uint64_t>(static_cast<const uint8_t*>(g.res) + (m0 * g.ldr + n0) * EB) : 0;
     // (readfirstlane returns int: each word goes through uint32_t before it
@@ -654,13 +653,15 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
       else
         static_assert(NR == 0, "pass shape");
     };
-    if (has_res) load_res(0);
+    if constexpr (has_res) load_res(0);
     compute(0);
     stage();
     read_back();
 #pragma unroll
     for (int t = 0; t < NP; ++t) {
-      if (has_res && t + 1 < NP) load_res(t + 1);
+      if constexpr (has_res) {
+        if (t + 1 < NP) load_res(t + 1);
+      }
       if (t + 1 < NP && (t + 1) % FM == 0) {
         // next column group: its scales replace this group's (already applied)
         load_sb((t + 1) / FM);
@@ -668,7 +669,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
       }
       if (t + 1 < NP) compute(t + 1);
       wait_reads();
-      if (has_res) add_res(t);
+      if constexpr (has_res) add_res(t);
       const int cg = t / FM, j = t % FM;
 #pragma unroll
       for (int rr = 0; rr < NR; ++rr)
@@ -900,7 +901,7 @@ constexpr int ring_slots() {
   return n > cap ? cap : n;
 }
 
-template <int BN, int BM, int OUT>
+template <int BN, int BM, int OUT, bool RES>
 static hipError_t launch_mfma(const GemmArgs& g, hipStream_t st) {
   constexpr int RB = tile_rb<BN, BM>();
   constexpr int NSL = ring_slots<BN, BM, RB>();
@@ -911,9 +912,9 @@ static hipError_t launch_mfma(const GemmArgs& g, hipStream_t st) {
   const int64_t kt = ((g.K + 2 * kBK - 1) / (2 * kBK)) * 2;
   const unsigned grid = static_cast<unsigned>(nt < cus || kt < NSL * (RB / kBK) ? nt : cus);
   if (g.K % (2 * kBK) == 0)
-    hipLaunchKernelGGL((gemm_fp8_mfma<BN, BM, NSL, RB, OUT, false>), dim3(grid), dim3(256), 0, st, g);
+    hipLaunchKernelGGL((gemm_fp8_mfma<BN, BM, NSL, RB, OUT, false, RES>), dim3(grid), dim3(256), 0, st, g);
   else
-    hipLaunchKernelGGL((gemm_fp8_mfma<BN, BM, NSL, RB, OUT, true>), dim3(grid), dim3(256), 0, st, g);
+    hipLaunchKernelGGL((gemm_fp8_mfma<BN, BM, NSL, RB, OUT, true, RES>), dim3(grid), dim3(256), 0, st, g);
   return hipGetLastError();
 }
 
@@ -946,10 +947,17 @@ static hipError_t dispatch(const GemmArgs& g, hipStream_t st) {
   };
   const double c256 = cost(256, 256, 1.0), c2561 = cost(256, 128, 0.9), c192 = cost(192, 128, 0.85),
                c128 = cost(128, 128, 0.7);
-  if (c256 <= c2561 && c256 <= c192 && c256 <= c128) return launch_mfma<256, 256, OUT>(g, st);
-  if (c2561 <= c192 && c2561 <= c128) return launch_mfma<256, 128, OUT>(g, st);
-  if (c192 <= c128) return launch_mfma<192, 128, OUT>(g, st);
-  return launch_mfma<128, 128, OUT>(g, st);
+  // the residual add is a variant of its own, so the plain kernels carry none
+  // of its code (measured 1-3 % on every tile shape when it was a runtime
+  // branch); only 16-bit outputs take a residual
+  constexpr bool kRes = OUT != FR_DTYPE_FP32;
+  if (c256 <= c2561 && c256 <= c192 && c256 <= c128)
+    return kRes && g.res ? launch_mfma<256, 256, OUT, kRes>(g, st) : launch_mfma<256, 256, OUT, false>(g, st);
+  if (c2561 <= c192 && c2561 <= c128)
+    return kRes && g.res ? launch_mfma<256, 128, OUT, kRes>(g, st) : launch_mfma<256, 128, OUT, false>(g, st);
+  if (c192 <= c128)
+    return kRes && g.res ? launch_mfma<192, 128, OUT, kRes>(g, st) : launch_mfma<192, 128, OUT, false>(g, st);
+  return kRes && g.res ? launch_mfma<128, 128, OUT, kRes>(g, st) : launch_mfma<128, 128, OUT, false>(g, st);
 }
 
 }  // namespace fr
