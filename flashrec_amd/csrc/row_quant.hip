@@ -341,6 +341,116 @@ __global__ __launch_bounds__(256) void row_kernel_vec(RowArgs a) {
   }
 }
 
+// Few rows (M up to a few per SIMD): one 256-thread workgroup per row, each
+// lane with NC chunks of 8 elements (chunk c at column (256 c + tid) * 8), the
+// row's sum of squares and amax reduced through LDS (wave partials summed in
+// wave order).  With one wave per row the per-lane arithmetic of a whole row
+// (about 10 ops per element) sits in a single wave's latency; here it is
+// spread over four.  Same arithmetic as row_kernel_vec but for the order of
+// the sum of squares.  quant, RMSNorm and add + RMSNorm; bf16 rows.
+template <int MODE, int NC, bool QOUT>
+__global__ __launch_bounds__(256) void row_kernel_split(RowArgs a) {
+  static_assert(MODE != kSilu, "split rows: quant and norm modes");
+  constexpr bool kNorm = MODE == kRms || MODE == kAddRms;
+  __shared__ float red[2][4];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int64_t row = blockIdx.x;
+  const int64_t K = a.K;
+  auto col = [&](int c) __attribute__((always_inline)) { return (static_cast<int64_t>(c) * 256 + tid) * 8; };
+  auto in = [&](int c) __attribute__((always_inline)) { return col(c) < K; };
+  const uint16_t* xr = a.x + row * a.ldx;
+  u32x4 xv[NC], uv[NC], wv[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    xv[c] = in(c) ? ldnt(reinterpret_cast<const u32x4*>(xr + col(c))) : u32x4{0, 0, 0, 0};
+    if (MODE == kAddRms)
+      uv[c] = in(c) ? ldnt(reinterpret_cast<const u32x4*>(a.res + row * a.ldr + col(c))) : u32x4{0, 0, 0, 0};
+    if (kNorm) wv[c] = in(c) ? *reinterpret_cast<const u32x4*>(a.w + col(c)) : u32x4{0, 0, 0, 0};
+  }
+  float v[NC][8];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    unpack8(xv[c], v[c]);
+    if (MODE == kAddRms) {
+      float r[8];
+      unpack8(uv[c], r);
+      u32x4 o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        o[i] = pack_bf16x2(r[2 * i] + v[c][2 * i], r[2 * i + 1] + v[c][2 * i + 1]);
+        v[c][2 * i] = __uint_as_float(o[i] << 16);
+        v[c][2 * i + 1] = __uint_as_float(o[i] & 0xFFFF0000u);
+      }
+      if (in(c)) stnt(reinterpret_cast<u32x4*>(a.res + row * a.ldr + col(c)), o);
+    }
+  }
+  if (kNorm) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(v[c][i], v[c][i], ss);
+    ss = wave_sum(ss);
+    if (lane == 0) red[0][wave] = ss;
+    __syncthreads();
+    ss = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
+    const float var = ss / static_cast<float>(K);
+    const float rstd = 1.0f / __builtin_sqrtf(var + a.eps);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      float w[8];
+      unpack8(wv[c], w);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[c][i] = (v[c][i] * rstd) * w[i];
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) round_bf16x2(v[c][i], v[c][i + 1]);
+    }
+  }
+  if (!QOUT) {
+    uint16_t* orow = reinterpret_cast<uint16_t*>(a.q) + row * a.ldq;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      if (in(c)) {
+        u32x4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = pack_bf16x2(v[c][2 * i], v[c][2 * i + 1]);
+        stnt(reinterpret_cast<u32x4*>(orow + col(c)), o);
+      }
+    }
+    return;
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = maxnan(amax, __builtin_fabsf(v[c][i]));
+  amax = wave_maxnan(amax);
+  if (lane == 0) red[1][wave] = amax;
+  __syncthreads();
+  amax = maxnan(maxnan(maxnan(red[1][0], red[1][1]), maxnan(red[1][2], red[1][3])), kAmaxFloor);
+  const float scale = amax / kFp8Max;
+  if (tid == 0) a.s[row] = scale;
+  uint8_t* qrow = a.q + row * a.ldq;
+  const bool finite = amax < 3.0e38f;
+  const float r = 1.0f / scale;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const u32x2 o = quant8_e4m3(v[c], scale, r, finite);
+    if (in(c)) stnt(reinterpret_cast<u32x2*>(qrow + col(c)), o);
+  }
+}
+
+template <int MODE, bool QOUT>
+static hipError_t launch_split(const RowArgs& a, hipStream_t st) {
+  const int64_t nc = (a.K + 2047) / 2048;
+  const dim3 grid(static_cast<unsigned>(a.M));
+  if (nc <= 1) hipLaunchKernelGGL((row_kernel_split<MODE, 1, QOUT>), grid, dim3(256), 0, st, a);
+  else if (nc <= 2) hipLaunchKernelGGL((row_kernel_split<MODE, 2, QOUT>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((row_kernel_split<MODE, 4, QOUT>), grid, dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
 // Several workgroups per CU; each wave walks rows with a grid stride (the
 // norm weight is unpacked once per wave).
 template <int MODE, bool QOUT, int NV>
@@ -364,6 +474,11 @@ static hipError_t launch_vec(const RowArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+// Row counts up to which a workgroup per row beats a wave per row (RMS->e4m3
+// at K = 2048, graph-replayed launches: 64 rows 3.48 -> 3.18 us, 256 rows
+// 3.99 -> 3.61, 512 rows 4.16 -> 3.97; 1024 rows 4.48 -> 4.66, slower).
+constexpr int64_t kSplitRowsMax = 512;
+
 template <int MODE, bool QOUT>
 static int launch_rows(RowArgs a, int dtype, hipStream_t st) {
   if (a.M < 0 || a.K < 0) return FR_EINVAL;
@@ -382,7 +497,9 @@ static int launch_rows(RowArgs a, int dtype, hipStream_t st) {
   if (QOUT) vec = vec && a.ldq % 8 == 0 && (reinterpret_cast<uintptr_t>(a.q) & 7u) == 0;
   else vec = vec && a.ldq % 8 == 0 && al16(a.q);
   hipError_t err;
-  if (vec) {
+  if (vec && MODE != kSilu && a.M <= kSplitRowsMax) {
+    err = launch_split<MODE == kSilu ? kQuant : MODE, QOUT>(a, st);
+  } else if (vec) {
     const int64_t nv = (K + 511) / 512;
     if (nv <= 1) err = launch_vec<MODE, QOUT, 1>(a, st);
     else if (nv <= 2) err = launch_vec<MODE, QOUT, 2>(a, st);
