@@ -423,7 +423,15 @@ def main() -> int:
                     help="only run 20 copies of a 256 MiB buffer (rocprof FETCH/WRITE_SIZE scale)")
     ap.add_argument("--mfma-ceiling", action="store_true",
                     help="only measure the fp8 MFMA rate on register operands (constant and random)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the config-4 decode step entries (for a kernel trace of the step)")
     args = ap.parse_args()
+    if args.decode_only:
+        from flashrec_amd._lib import load
+
+        load()
+        print(json.dumps(_decode_step_case(torch.device("cuda:0"))))
+        return 0
     if args.mfma_ceiling:
         from flashrec_amd._lib import load
 
