@@ -84,19 +84,37 @@ __device__ __forceinline__ bool cand_ok(const GenrecArgs& a, int64_t node, int64
   return a.allow[safe * a.vsz + rel] != 0;
 }
 
-// Output i of merge(A[0..na), B[0..nb)), both descending.
-__device__ __forceinline__ uint64_t merge_at(const uint64_t* A, int na, const uint64_t* B, int nb, int i) {
-  int lo = i - nb > 0 ? i - nb : 0;
-  int hi = i < na ? i : na;
+// Outputs i0 .. i0 + count - 1 of merge(A[0..na), B[0..nb)), both
+// descending, into dst[i0 ..]: one
+// binary search for where output i0 splits A and B (merge path), then a
+// sequential walk, one comparison per output with the two heads in
+// registers.
+__device__ __forceinline__ void merge_run(const uint64_t* A, int na, const uint64_t* B, int nb, int i0, int count,
+                                          uint64_t* dst) {
+  int lo = i0 - nb > 0 ? i0 - nb : 0;
+  int hi = i0 < na ? i0 : na;
   while (lo < hi) {
     const int mid = (lo + hi) >> 1;
-    if (A[mid] > B[i - mid - 1]) lo = mid + 1;
+    if (A[mid] > B[i0 - mid - 1]) lo = mid + 1;
     else hi = mid;
   }
-  const int j = lo;
-  const bool take_a = j < na && (i - j >= nb || A[j] > B[i - j]);
-  return take_a ? A[j] : B[i - j];
+  int ia = lo, ib = i0 - lo;
+  uint64_t ha = ia < na ? A[ia] : 0, hb = ib < nb ? B[ib] : 0;
+  for (int k = 0; k < count; ++k) {
+    const bool take_a = ia < na && (ib >= nb || ha > hb);
+    if (take_a) {
+      dst[i0 + k] = ha;
+      ++ia;
+      ha = ia < na ? A[ia] : 0;
+    } else {
+      dst[i0 + k] = hb;
+      ++ib;
+      hb = ib < nb ? B[ib] : 0;
+    }
+  }
 }
+
+constexpr int kRun = 8;  // outputs per thread per merge_run
 
 // Merge `n` lists (list l at src + l * K, length len[l]) pairwise down to
 // one, ping-ponging between src and dst; returns the buffer holding it (at
@@ -104,11 +122,14 @@ __device__ __forceinline__ uint64_t merge_at(const uint64_t* A, int na, const ui
 __device__ uint64_t* merge_tree(uint64_t* src, uint64_t* dst, int* len, int n, int K) {
   while (n > 1) {
     const int pairs = n >> 1;
-    const int total = pairs * K;
-    for (int t = threadIdx.x; t < total; t += blockDim.x) {
-      const int p = t / K, i = t - p * K;
+    const int runs = (K + kRun - 1) / kRun;  // per pair
+    for (int t = threadIdx.x; t < pairs * runs; t += blockDim.x) {
+      const int p = t / runs, i0 = (t - p * runs) * kRun;
       const int la = len[2 * p], lb = len[2 * p + 1];
-      if (i < la + lb && i < K) dst[p * K + i] = merge_at(src + 2 * p * K, la, src + (2 * p + 1) * K, lb, i);
+      const int lim = la + lb < K ? la + lb : K;
+      if (i0 < lim)
+        merge_run(src + 2 * p * K, la, src + (2 * p + 1) * K, lb, i0, lim - i0 < kRun ? lim - i0 : kRun,
+                  dst + p * K);
     }
     // an odd list out is carried over unchanged
     if (n & 1)
@@ -130,7 +151,9 @@ __device__ uint64_t* merge_tree(uint64_t* src, uint64_t* dst, int* len, int n, i
   return src;
 }
 
-__global__ __launch_bounds__(256) void genrec_slice_topk(GenrecArgs a) {
+constexpr int kSliceWaves = 16;  // one wave per beam of a slice (BS <= 16)
+
+__global__ __launch_bounds__(64 * kSliceWaves) void genrec_slice_topk(GenrecArgs a) {
   __shared__ uint64_t bufA[kListKeys];
   __shared__ uint64_t bufB[kListKeys];
   __shared__ int len[64];
@@ -139,29 +162,49 @@ __global__ __launch_bounds__(256) void genrec_slice_topk(GenrecArgs a) {
   const int b0 = s * a.BS;
   const int nb = a.BW - b0 < a.BS ? a.BW - b0 : a.BS;
   const bool mask = a.apply_mask && a.allow != nullptr && a.nodes != nullptr;
-  // each wave compacts beams wave, wave + 4, ...: list of beam j at bufA + j * K
-  for (int j = wave; j < nb; j += 4) {
+  // each wave compacts beams wave, wave + kSliceWaves, ... (one each when
+  // BS <= kSliceWaves): list of beam j at bufA + j * K.
+  // A beam's candidates go in groups of kPre chunks of 64: the scores and
+  // tokens of the whole group are loaded, then all of its trie lookups are
+  // issued, then the chunks are compacted in order (ballot prefix sums,
+  // stopping at K): two memory round trips per group instead of two per
+  // chunk.  Which candidates are taken, and where, is unchanged.
+  constexpr int kPre = 16;
+  for (int j = wave; j < nb; j += kSliceWaves) {
     const int b = b0 + j;
     const float cb = a.cum[static_cast<int64_t>(n) * a.BW + b];
     const int64_t node = mask ? a.nodes[static_cast<int64_t>(n) * a.BW + b] : -1;
     const float* lpb = a.lp + (static_cast<int64_t>(n) * a.BW + b) * a.C;
     const int64_t* tkb = a.tok + (static_cast<int64_t>(n) * a.BW + b) * a.C;
     int count = 0;
-    for (int c0 = 0; c0 < a.C && count < a.K; c0 += 64) {
-      const int c = c0 + lane;
-      bool ok = false;
-      float v = 0.0f;
-      if (c < a.C) {
-        v = cb + lpb[c];
-        ok = v == v;  // NaN: never picked
-        if (mask) ok = ok && v != a.neg_inf && cand_ok(a, node, tkb[c]);
+    for (int g0 = 0; g0 < a.C && count < a.K; g0 += 64 * kPre) {
+      float v[kPre];
+      int64_t tk[kPre];
+#pragma unroll
+      for (int u = 0; u < kPre; ++u) {
+        const int c = g0 + 64 * u + lane;
+        v[u] = c < a.C ? cb + lpb[c] : 0.0f;
+        tk[u] = c < a.C && mask ? tkb[c] : 0;
       }
-      const uint64_t bal = __ballot(ok);
-      const int pos = count + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
-                                  static_cast<uint32_t>(bal >> 32),
-                                  __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u)));
-      if (ok && pos < a.K) bufA[j * a.K + pos] = make_key(v, static_cast<uint32_t>(b * a.C + c));
-      count += __builtin_popcountll(bal);
+      bool okv[kPre];
+#pragma unroll
+      for (int u = 0; u < kPre; ++u) {
+        const int c = g0 + 64 * u + lane;
+        bool ok = c < a.C && v[u] == v[u];  // NaN: never picked
+        if (mask) ok = ok && v[u] != a.neg_inf && cand_ok(a, node, tk[u]);
+        okv[u] = ok;
+      }
+#pragma unroll
+      for (int u = 0; u < kPre; ++u) {
+        if (count >= a.K) break;
+        const int c = g0 + 64 * u + lane;
+        const uint64_t bal = __ballot(okv[u]);
+        const int pos = count + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+                                    static_cast<uint32_t>(bal >> 32),
+                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u)));
+        if (okv[u] && pos < a.K) bufA[j * a.K + pos] = make_key(v[u], static_cast<uint32_t>(b * a.C + c));
+        count += __builtin_popcountll(bal);
+      }
     }
     if (lane == 0) len[j] = count < a.K ? count : a.K;
   }
@@ -183,39 +226,40 @@ __global__ __launch_bounds__(1024) void genrec_request_topk_expand(GenrecArgs a)
   const int n = blockIdx.x;
   const int K = a.K;
   const uint64_t* lists = a.scratch + static_cast<int64_t>(n) * a.S * (1 + K);
-  // The slice lists go in groups of G (G / 2 merged pairs fill an LDS
-  // buffer); each group is merged down to one list and folded into acc.
-  const int G = 2 * (kListKeys / K);
+  // The slice lists go in groups of G that fill an LDS buffer: a group is
+  // copied in (coalesced, one memory round trip), merged down to one list
+  // in LDS and folded into acc.  (Merging straight from the scratch would
+  // put a dependent global read at every step of every binary search.)
+  const int G = kListKeys / K < 64 ? kListKeys / K : 64;  // (len[] holds 64)
   if (threadIdx.x == 0) acc_len = 0;
   for (int g0 = 0; g0 < a.S; g0 += G) {
     const int gs = a.S - g0 < G ? a.S - g0 : G;
     const uint64_t* gl = lists + static_cast<int64_t>(g0) * (1 + K);
-    const int pairs = gs >> 1;
-    const int m = pairs + (gs & 1);
-    for (int t = threadIdx.x; t < pairs * K; t += blockDim.x) {
-      const int p = t / K, i = t - p * K;
-      const uint64_t* A = gl + (2 * p) * (1 + K);
-      const uint64_t* B = gl + (2 * p + 1) * (1 + K);
-      const int la = static_cast<int>(A[0]), lb = static_cast<int>(B[0]);
-      if (i < la + lb) bufA[p * K + i] = merge_at(A + 1, la, B + 1, lb, i);
+    if (threadIdx.x < gs) len[threadIdx.x] = static_cast<int>(gl[static_cast<int64_t>(threadIdx.x) * (1 + K)]);
+    __syncthreads();
+    // the keys of every list of the group (gs * K <= kListKeys = 8 per
+    // thread of 1024): all loads issued before any is stored
+    constexpr int kPer = kListKeys / 1024;
+    uint64_t key[kPer];
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+      const int t = threadIdx.x + r * 1024;
+      const int l = t / K, i = t - l * K;
+      key[r] = (l < gs && i < len[l]) ? gl[static_cast<int64_t>(l) * (1 + K) + 1 + i] : 0;
     }
-    if (gs & 1) {
-      const uint64_t* A = gl + (gs - 1) * (1 + K);
-      for (int i = threadIdx.x; i < static_cast<int>(A[0]); i += blockDim.x) bufA[pairs * K + i] = A[1 + i];
-    }
-    if (threadIdx.x == 0) {
-      for (int p = 0; p < pairs; ++p) {
-        const int s = static_cast<int>(gl[(2 * p) * (1 + K)] + gl[(2 * p + 1) * (1 + K)]);
-        len[p] = s < K ? s : K;
-      }
-      if (gs & 1) len[pairs] = static_cast<int>(gl[(gs - 1) * (1 + K)]);
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+      const int t = threadIdx.x + r * 1024;
+      const int l = t / K, i = t - l * K;
+      if (l < gs && i < len[l]) bufA[l * K + i] = key[r];
     }
     __syncthreads();
-    uint64_t* res = merge_tree(bufA, bufB, len, m, K);
+    uint64_t* res = merge_tree(bufA, bufB, len, gs, K);
     uint64_t* other = res == bufA ? bufB : bufA;
     const int lr = len[0], la = acc_len;
     const int lt = la + lr < K ? la + lr : K;
-    for (int i = threadIdx.x; i < lt; i += blockDim.x) other[i] = merge_at(acc, la, res, lr, i);
+    for (int i0 = threadIdx.x * kRun; i0 < lt; i0 += blockDim.x * kRun)
+      merge_run(acc, la, res, lr, i0, lt - i0 < kRun ? lt - i0 : kRun, other);
     __syncthreads();
     for (int i = threadIdx.x; i < lt; i += blockDim.x) acc[i] = other[i];
     if (threadIdx.x == 0) acc_len = lt;
@@ -361,7 +405,7 @@ static int genrec_launch(
   a.apply_expand = apply_expand;
   a.apply_advance = apply_advance;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(genrec_slice_topk, dim3(static_cast<unsigned>(N * a.S)), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(genrec_slice_topk, dim3(static_cast<unsigned>(N * a.S)), dim3(64 * kSliceWaves), 0, st, a);
   hipLaunchKernelGGL(genrec_request_topk_expand, dim3(static_cast<unsigned>(N)), dim3(1024), 0, st, a);
   return hipGetLastError() == hipSuccess ? FR_OK : FR_ELAUNCH;
 }

@@ -66,7 +66,7 @@ def test_config4_shape(dev):
 
 
 @pytest.mark.parametrize("n,bw,c,k", [(3, 50, 100, 50), (2, 37, 65, 20), (1, 16, 64, 1000), (4, 200, 7, 130),
-                                      (2, 512, 1024, 1024)])
+                                      (2, 512, 1024, 1024), (1, 2048, 16, 32), (2, 1100, 8, 8)])
 def test_shapes(dev, n, bw, c, k):
     _compare(dev, _case(n, bw, c, 300, 40, 0.5, n * 7 + bw), k)
 
