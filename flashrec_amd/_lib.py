@@ -48,6 +48,7 @@ SIGNATURES = {
     "fr_fp8_scaled_mm": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I32, _P],
     "fr_fp8_scaled_mm_residual": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64,
                                   _I32, _P],
+    "fr_fp8_scaled_mm_silu": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P],
     "fr_qk_norm_rope_store_fp8": [
         _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,  # q, k, v + strides
         _P, _P, _P, _P, _F32, _P, _I64,  # pos, loc, qw, kw, eps, cos_sin, rows

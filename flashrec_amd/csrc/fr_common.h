@@ -64,6 +64,30 @@ __device__ __forceinline__ float round_bf16(float x) {
   return bf16_to_f32(static_cast<uint16_t>(pack_bf16x2(x, 0.0f) & 0xFFFFu));
 }
 
+// Pairs of bf16 roundings with one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ void round_bf16x2(float& a, float& b) {
+  const uint32_t w = pack_bf16x2(a, b);
+  a = __uint_as_float(w << 16);
+  b = __uint_as_float(w & 0xFFFF0000u);
+}
+
+// silu(g) = g / (1 + exp(-g)) for |g| <= 80 (the result is rounded to bf16
+// next).  exp(-g) = 2^a with a = fl(-g * log2(e)); the quotient by
+// d = 1 + 2^a is corrected as in div_rn_shared.  The one inexact step left is
+// the rounding of a, which moves 2^a by at most |a| * 2^-24 * ln 2 relative:
+// with the hardware exp2, under 3 fp32 ulps for |g| <= 4; for g < -4 up to
+// |g| * 6e-8 relative, on results below 0.08 in magnitude.  Against the reference's bf16 results this
+// flipped no output on N(0, s^2) rows with s = 1, 4 and 20 (the variant that
+// also carries a's rounding error, 4 more operations per element, agrees
+// bit for bit and is 7 % slower).  In range, 2^a and d are finite and
+// positive.
+__device__ __forceinline__ float silu_in_range(float g) {
+  const float d = 1.0f + __builtin_amdgcn_exp2f(g * -1.4426950216293335f);
+  const float r = __builtin_amdgcn_rcpf(d);
+  const float y = g * r;
+  return __builtin_fmaf(-__builtin_fmaf(y, d, -g), r, y);
+}
+
 __device__ __forceinline__ float fp16_to_f32(uint16_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }

@@ -59,9 +59,15 @@ struct GemmArgs {
   // product: out = rnd(rnd(product) + res); may alias out (same ldo), or null
   const void* res;
   int64_t ldr;
+  // SiLU-and-mul epilogue: out is [M, N / 2] bf16 (see gemm_fp8_mfma)
+  int silu;
 };
 
 constexpr int kBK = 64;  // bytes of K per MFMA step
+// Epilogue variants (a compile-time kernel parameter, so the plain kernels
+// carry none of the others' code): the scaled product; the same plus a
+// residual added after rounding; SiLU-and-mul of gate/up column pairs.
+constexpr int kEpiPlain = 0, kEpiRes = 1, kEpiSilu = 2;
 constexpr int kNT = 2;   // buffer-instruction cache policy bit: nontemporal (gfx950)
 
 // LDS rows are 64 bytes (4 chunks of 16 B); chunk c of row r lives in slot
@@ -255,8 +261,8 @@ __device__ __forceinline__ void tile_coords(int64_t pid, int64_t nt, int64_t til
 // RB: bytes of K per LDS row (64: one MFMA K step per ring slot, 128: two,
 // so each direct-to-LDS load covers whole 128-byte lines), NSL: ring depth
 // in slots, KTAIL: K % 128 != 0 (the last K steps are partly or wholly
-// zero-filled).
-template <int BN, int BM, int NSL, int RB, int OUT, bool KTAIL, bool RES>
+// zero-filled).  EPI: kEpiPlain, kEpiRes or kEpiSilu.
+template <int BN, int BM, int NSL, int RB, int OUT, bool KTAIL, int EPI>
 __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   // The host pass only needs the kernel's signature (for its launch stub);
   // the body uses device-only buffer-resource builtins.
@@ -273,6 +279,13 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   constexpr int STAGE = (BN + BM) * RB;
   constexpr int LOADS = IB + IA;  // vmcnt units one slot adds per wave
   constexpr int EB = OutT<OUT>::kBytes;
+  constexpr bool RES = EPI == kEpiRes;
+  // SiLU-and-mul (bf16 only): the weight rows come in chunks of 16, the
+  // gate rows of 8 output columns followed by their 8 up rows; the product
+  // column c of chunk k is bf16(bf16(silu(gate)) * up) of chunk columns c
+  // and 8 + c, written at output column 8k + c (the output is N / 2 wide).
+  constexpr bool SILU = EPI == kEpiSilu;
+  static_assert(!SILU || OUT == FR_DTYPE_BF16, "SiLU epilogue writes bf16");
   // LDS: the slot ring, two 2 KB scale buffers, per-wave epilogue staging of
   // 32 rows x 128 bytes, or x 64 bytes where the wider staging does not fit
   // (narrow also when a wave's columns are not whole 128-byte staging rows:
@@ -443,7 +456,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
   // measured in one process against the staged form, they were 1-12 %
   // slower on every tile shape.
   // stores per wave per tile on the fast paths (fp32: 16 bytes per (i, j, q))
-  constexpr int kStagedStores = OUT == FR_DTYPE_FP32 ? 4 * FN * FM : 2 * FN * FM;
+  constexpr int kStagedStores = OUT == FR_DTYPE_FP32 ? 4 * FN * FM : (SILU ? FN * FM : 2 * FN * FM);
   // Returns whether a fast path ran (and so issued exactly kStagedStores
   // stores per wave).
   auto epilogue = [&](int64_t local) -> bool __attribute__((always_inline)) {
@@ -460,6 +473,35 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
                                 (reinterpret_cast<uintptr_t>(g.res) & 15) == 0 && g.ldr < (int64_t(1) << 22))) &&
                       (g.ldo * EB) % 16 == 0 && (reinterpret_cast<uintptr_t>(g.out) & 15) == 0 &&
                       g.ldo < (int64_t(1) << 22);  // tile offsets fit the 32-bit store offsets
+    if (!fast && SILU) {
+      // gate columns n .. n+3 and their up columns n+8 .. n+11 (N is a
+      // multiple of 16, so a chunk is never cut by the edge)
+      const int ls = lane_id_here();
+      uint16_t* const o16 = static_cast<uint16_t*>(g.out);
+#pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        const int64_t m = m0 + j * 32 + (ls & 31);
+        if (m >= g.M) continue;
+        const float sam = g.sa[m * g.sa_stride];
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+          for (int q = 0; q < 4; q += 2) {
+            const int64_t n = n0 + i * 32 + 8 * q + 4 * (ls >> 5);
+            if (n >= g.N) continue;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              const float gt = round_bf16((acc[i][j][4 * q + t] * sam) * g.sb[(n + t) * g.sb_stride]);
+              const float up = round_bf16((acc[i][j][4 * q + 4 + t] * sam) * g.sb[(n + 8 + t) * g.sb_stride]);
+              const float sg = __builtin_fabsf(gt) <= 80.0f ? silu_in_range(gt) : gt / (1.0f + expf(-gt));
+              o16[m * g.ldo + (n / 16) * 8 + 4 * (ls >> 5) + t] =
+                  static_cast<uint16_t>(pack_bf16x2(round_bf16(sg) * up, 0.0f) & 0xFFFFu);
+            }
+          }
+      }
+      waitcnt_vm<0>();
+      return false;
+    }
     if (!fast) {
       const int ls = lane_id_here();
 #pragma unroll
@@ -513,24 +555,35 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     constexpr int RPL = 256 / SRB;       // staging rows per 256-byte LDS bank line
     constexpr int RPR = 64 / CPRS;       // rows per read-back instruction
     constexpr int NR = 32 / RPR;         // read-backs (and stores) per pass
-    static_assert(NP * NR == kStagedStores, "store count per tile");
+    // Output side of a pass: the same, except that SiLU passes write half
+    // as many columns (CPPO), staged in rows of SRBO bytes.
+    constexpr int OD = SILU ? 2 : 1;
+    constexpr int CPPO = CPP / OD;
+    constexpr int NQO = NQ / OD;
+    constexpr int SRBO = CPPO * EB;
+    constexpr int CPRSO = SRBO / 16;
+    constexpr int RPLO = 256 / SRBO;
+    constexpr int RPRO = 64 / CPRSO;
+    constexpr int NRO = 32 / RPRO;
+    static_assert(!SILU || CPP % 16 == 0, "SiLU passes hold whole gate/up chunks");
+    static_assert(NP * NRO == kStagedStores, "store count per tile");
     using PkT = typename std::conditional<EB == 4, u32x4, u32x2>::type;
     const uint32_t stg_base = lds_addr(stg);
     // stores through a buffer resource based at this wave's sub-tile: the
     // lane's offset is formed once, each store's row/column step is a scalar
     // offset (no 64-bit address arithmetic per store)
-    const uint64_t obase = reinterpret_cast<uint64_t>(static_cast<uint8_t*>(g.out) + (m0 * g.ldo + n0) * EB);
+    const uint64_t obase = reinterpret_cast<uint64_t>(static_cast<uint8_t*>(g.out) + (m0 * g.ldo + n0 / OD) * EB);
     const uint32_t olo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(obase));
     const uint32_t ohi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(obase >> 32));
     const __amdgpu_buffer_rsrc_t ro =
         make_rsrc(reinterpret_cast<const void*>((static_cast<uint64_t>(ohi) << 32) | olo), 0xFFFFFFFFu);
     const uint32_t ldo32 = static_cast<uint32_t>(g.ldo);
-    const uint32_t vo = ((lx / CPRS) * ldo32 + (lx % CPRS) * (16 / EB)) * EB;
-    uint32_t ra[NR];
+    const uint32_t vo = ((lx / CPRSO) * ldo32 + (lx % CPRSO) * (16 / EB)) * EB;
+    uint32_t ra[NRO];
 #pragma unroll
-    for (int rr = 0; rr < NR; ++rr) {
-      const int r = rr * RPR + lx / CPRS;
-      ra[rr] = stg_base + r * SRB + (((lx % CPRS) ^ ((r / RPL) % CPRS)) << 4);
+    for (int rr = 0; rr < NRO; ++rr) {
+      const int r = rr * RPRO + lx / CPRSO;
+      ra[rr] = stg_base + r * SRBO + (((lx % CPRSO) ^ ((r / RPLO) % CPRSO)) << 4);
     }
     // scales: sa of the wave's rows up front, sb per column group
     u32x4 sb4[NQ];
@@ -556,9 +609,50 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
       sam_r[j] = sa_vec ? (kSafeReads ? lds_read_f32_wait(sal + 128 * j) : lds_read_f32_nw(sal + 128 * j)) : sa0;
     load_sb(0);
     lds_wait_all(sb4, sam_r);
-    PkT pk[NQ];
+    PkT pk[NQO];
     auto compute = [&](int t) __attribute__((always_inline)) {
       const int cg = t / FM, j = t % FM;
+      if constexpr (SILU) {
+        // 8-column groups 2k (gate) and 2k + 1 (up) of the pass are one chunk
+        float gt[NQO][4], up[NQO][4], sg[NQO][4];
+        bool wide = false;
+#pragma unroll
+        for (int k = 0; k < NQO; ++k) {
+          const int col = cg * CPP + 16 * k;
+          const int i = col / 32, q = (col % 32) / 8;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            gt[k][e] = (acc[i][j][4 * q + e] * sam_r[j]) * __uint_as_float(sb4[2 * k][e]);
+            up[k][e] = (acc[i][j][4 * q + 4 + e] * sam_r[j]) * __uint_as_float(sb4[2 * k + 1][e]);
+          }
+#pragma unroll
+          for (int e = 0; e < 4; e += 2) {
+            round_bf16x2(gt[k][e], gt[k][e + 1]);
+            round_bf16x2(up[k][e], up[k][e + 1]);
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            wide = wide || !(__builtin_fabsf(gt[k][e]) <= 80.0f);
+            sg[k][e] = silu_in_range(gt[k][e]);
+          }
+        }
+        // gates beyond the in-range form (|g| > 80, inf, NaN): torch's formula
+        if (__builtin_expect(__ballot(wide) != 0, 0)) {
+#pragma unroll
+          for (int k = 0; k < NQO; ++k)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (!(__builtin_fabsf(gt[k][e]) <= 80.0f)) sg[k][e] = gt[k][e] / (1.0f + expf(-gt[k][e]));
+        }
+#pragma unroll
+        for (int k = 0; k < NQO; ++k) {
+          round_bf16x2(sg[k][0], sg[k][1]);
+          round_bf16x2(sg[k][2], sg[k][3]);
+          pk[k][0] = pack_bf16x2(sg[k][0] * up[k][0], sg[k][1] * up[k][1]);
+          pk[k][1] = pack_bf16x2(sg[k][2] * up[k][2], sg[k][3] * up[k][3]);
+        }
+        return;
+      }
 #pragma unroll
       for (int u = 0; u < NQ; ++u) {
         const int col = cg * CPP + 8 * u;
@@ -577,14 +671,14 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     };
     auto stage = [&]() __attribute__((always_inline)) {
 #pragma unroll
-      for (int u = 0; u < NQ; ++u) {
+      for (int u = 0; u < NQO; ++u) {
         const int byte = (8 * u + h4) * EB;  // inside the staging row
-        const uint32_t ad = stg_base + row * SRB + ((((byte >> 4) ^ ((row / RPL) % CPRS))) << 4) + (byte & 15);
+        const uint32_t ad = stg_base + row * SRBO + ((((byte >> 4) ^ ((row / RPLO) % CPRSO))) << 4) + (byte & 15);
         if constexpr (EB == 4) lds_write_b128(ad, pk[u]);
         else lds_write_b64(ad, pk[u][0], pk[u][1]);
       }
     };
-    u32x4 w[NR];
+    u32x4 w[NRO];
     // residual rows (16-bit outputs): read with the same segment layout as
     // the stores, one pass ahead, and added to the converted product
     constexpr bool has_res = RES && kResFast && EB == 2;
@@ -627,32 +721,34 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
     };
     auto read_back = [&]() __attribute__((always_inline)) {
 #pragma unroll
-      for (int rr = 0; rr < NR; ++rr) w[rr] = kSafeReads ? lds_read_b128_wait(ra[rr]) : lds_read_b128_nw(ra[rr]);
+      for (int rr = 0; rr < NRO; ++rr) w[rr] = kSafeReads ? lds_read_b128_wait(ra[rr]) : lds_read_b128_nw(ra[rr]);
     };
     // one wait for the reads, taking the next pass's values as operands so
     // their arithmetic stays ahead of it
     auto wait_reads = [&]() __attribute__((always_inline)) {
-      if constexpr (NR == 4 && NQ == 8)
+      if constexpr (NRO == 4 && NQO == 8)
         asm volatile("s_waitcnt lgkmcnt(0)"
                      : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(pk[0]), "+v"(pk[1]), "+v"(pk[2]),
                        "+v"(pk[3]), "+v"(pk[4]), "+v"(pk[5]), "+v"(pk[6]), "+v"(pk[7])
                      :
                      : "memory");
-      else if constexpr (NR == 4 && NQ == 4)
+      else if constexpr (NRO == 4 && NQO == 4)
         asm volatile("s_waitcnt lgkmcnt(0)"
                      : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(pk[0]), "+v"(pk[1]), "+v"(pk[2]),
                        "+v"(pk[3])
                      :
                      : "memory");
-      else if constexpr (NR == 2 && NQ == 4)
+      else if constexpr (NRO == 2 && NQO == 4)
         asm volatile("s_waitcnt lgkmcnt(0)"
                      : "+v"(w[0]), "+v"(w[1]), "+v"(pk[0]), "+v"(pk[1]), "+v"(pk[2]), "+v"(pk[3])
                      :
                      : "memory");
-      else if constexpr (NR == 2 && NQ == 2)
+      else if constexpr (NRO == 2 && NQO == 2)
         asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(w[0]), "+v"(w[1]), "+v"(pk[0]), "+v"(pk[1]) : : "memory");
+      else if constexpr (NRO == 1 && NQO == 2)
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(w[0]), "+v"(pk[0]), "+v"(pk[1]) : : "memory");
       else
-        static_assert(NR == 0, "pass shape");
+        static_assert(NRO == 0, "pass shape");
     };
     if constexpr (has_res) load_res(0);
     compute(0);
@@ -676,9 +772,9 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
       // not read back by this kernel; 2-3 % faster on the 4096-row gate_up,
       // down and M = 512 shapes, the decode step unchanged
 #pragma unroll
-      for (int rr = 0; rr < NR; ++rr)
+      for (int rr = 0; rr < NRO; ++rr)
         __builtin_amdgcn_raw_buffer_store_b128(w[rr], ro, vo,
-                                               static_cast<int>(((j * 32 + rr * RPR) * ldo32 + cg * CPP) * EB), kNT);
+                                               static_cast<int>(((j * 32 + rr * RPRO) * ldo32 + cg * CPPO) * EB), kNT);
       if (t + 1 < NP) {
         stage();
         read_back();
@@ -905,7 +1001,7 @@ constexpr int ring_slots() {
   return n > cap ? cap : n;
 }
 
-template <int BN, int BM, int OUT, bool RES>
+template <int BN, int BM, int OUT, int EPI>
 static hipError_t launch_mfma(const GemmArgs& g, hipStream_t st) {
   constexpr int RB = tile_rb<BN, BM>();
   constexpr int NSL = ring_slots<BN, BM, RB>();
@@ -916,9 +1012,9 @@ static hipError_t launch_mfma(const GemmArgs& g, hipStream_t st) {
   const int64_t kt = ((g.K + 2 * kBK - 1) / (2 * kBK)) * 2;
   const unsigned grid = static_cast<unsigned>(nt < cus || kt < NSL * (RB / kBK) ? nt : cus);
   if (g.K % (2 * kBK) == 0)
-    hipLaunchKernelGGL((gemm_fp8_mfma<BN, BM, NSL, RB, OUT, false, RES>), dim3(grid), dim3(256), 0, st, g);
+    hipLaunchKernelGGL((gemm_fp8_mfma<BN, BM, NSL, RB, OUT, false, EPI>), dim3(grid), dim3(256), 0, st, g);
   else
-    hipLaunchKernelGGL((gemm_fp8_mfma<BN, BM, NSL, RB, OUT, true, RES>), dim3(grid), dim3(256), 0, st, g);
+    hipLaunchKernelGGL((gemm_fp8_mfma<BN, BM, NSL, RB, OUT, true, EPI>), dim3(grid), dim3(256), 0, st, g);
   return hipGetLastError();
 }
 
@@ -951,17 +1047,27 @@ static hipError_t dispatch(const GemmArgs& g, hipStream_t st) {
   };
   const double c256 = cost(256, 256, 1.0), c2561 = cost(256, 128, 0.9), c192 = cost(192, 128, 0.85),
                c128 = cost(128, 128, 0.7);
-  // the residual add is a variant of its own, so the plain kernels carry none
-  // of its code (measured 1-3 % on every tile shape when it was a runtime
-  // branch); only 16-bit outputs take a residual
-  constexpr bool kRes = OUT != FR_DTYPE_FP32;
+  // the residual add and SiLU-and-mul are variants of their own, so the
+  // plain kernels carry none of their code (measured 1-3 % on every tile
+  // shape when the residual was a runtime branch); only 16-bit outputs take
+  // a residual, only bf16 takes SiLU (never on the 192-column tile, whose
+  // wave sub-tiles are not whole gate/up chunk pairs)
+  if constexpr (OUT == FR_DTYPE_BF16) {
+    if (g.silu) {
+      if (c256 <= c2561 && c256 <= c128) return launch_mfma<256, 256, OUT, kEpiSilu>(g, st);
+      if (c2561 <= c128) return launch_mfma<256, 128, OUT, kEpiSilu>(g, st);
+      return launch_mfma<128, 128, OUT, kEpiSilu>(g, st);
+    }
+  }
+  constexpr int kRes = OUT != FR_DTYPE_FP32 ? kEpiRes : kEpiPlain;
+  const bool res = OUT != FR_DTYPE_FP32 && g.res;
   if (c256 <= c2561 && c256 <= c192 && c256 <= c128)
-    return kRes && g.res ? launch_mfma<256, 256, OUT, kRes>(g, st) : launch_mfma<256, 256, OUT, false>(g, st);
+    return res ? launch_mfma<256, 256, OUT, kRes>(g, st) : launch_mfma<256, 256, OUT, kEpiPlain>(g, st);
   if (c2561 <= c192 && c2561 <= c128)
-    return kRes && g.res ? launch_mfma<256, 128, OUT, kRes>(g, st) : launch_mfma<256, 128, OUT, false>(g, st);
+    return res ? launch_mfma<256, 128, OUT, kRes>(g, st) : launch_mfma<256, 128, OUT, kEpiPlain>(g, st);
   if (c192 <= c128)
-    return kRes && g.res ? launch_mfma<192, 128, OUT, kRes>(g, st) : launch_mfma<192, 128, OUT, false>(g, st);
-  return kRes && g.res ? launch_mfma<128, 128, OUT, kRes>(g, st) : launch_mfma<128, 128, OUT, false>(g, st);
+    return res ? launch_mfma<192, 128, OUT, kRes>(g, st) : launch_mfma<192, 128, OUT, kEpiPlain>(g, st);
+  return res ? launch_mfma<128, 128, OUT, kRes>(g, st) : launch_mfma<128, 128, OUT, kEpiPlain>(g, st);
 }
 
 }  // namespace fr
@@ -971,11 +1077,11 @@ using namespace fr;
 static int gemm_entry(const void* a, int64_t lda, const void* b, int64_t ldb, const float* scale_a,
                       int64_t scale_a_numel, const float* scale_b, int64_t scale_b_numel, const void* bias,
                       int64_t bias_numel, const void* res, int64_t ldr, void* out, int64_t ldo, int64_t M,
-                      int64_t N, int64_t K, int out_dtype, void* stream) {
+                      int64_t N, int64_t K, int out_dtype, void* stream, bool silu = false) {
   if (M < 0 || N < 0 || K < 0) return FR_EINVAL;
   if (M == 0 || N == 0) return FR_OK;
   if (!a || !b || !scale_a || !scale_b || !out) return FR_EINVAL;
-  if (lda < K || ldb < K || ldo < N) return FR_EINVAL;
+  if (lda < K || ldb < K || ldo < (silu ? N / 2 : N)) return FR_EINVAL;
   if (!(scale_a_numel == 1 || scale_a_numel == M)) return FR_EINVAL;
   if (!(scale_b_numel == 1 || scale_b_numel == N)) return FR_EINVAL;
   if (bias && bias_numel != N) return FR_EINVAL;  // the epilogue reads bias[0..N)
@@ -997,6 +1103,7 @@ static int gemm_entry(const void* a, int64_t lda, const void* b, int64_t ldb, co
   g.K = K;
   g.res = res;
   g.ldr = ldr;
+  g.silu = silu ? 1 : 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t err;
   switch (out_dtype) {
@@ -1029,4 +1136,21 @@ extern "C" int fr_fp8_scaled_mm_residual(const void* a, int64_t lda, const void*
   if (residual == out && ldr != ldo) return FR_EINVAL;
   return gemm_entry(a, lda, b, ldb, scale_a, scale_a_numel, scale_b, scale_b_numel, nullptr, 0, residual, ldr, out,
                     ldo, M, N, K, out_dtype, stream);
+}
+
+// out[m, 8k + c] = bf16(bf16(silu(p[m, 16k + c])) * p[m, 16k + 8 + c]) for
+// the bf16-rounded scaled product p (c < 8): SiLU-and-mul in the epilogue,
+// with the weight rows given in gate/up chunks of 8 (see gemm_fp8_mfma).
+extern "C" int fr_fp8_scaled_mm_silu(const void* a, int64_t lda, const void* b, int64_t ldb, const float* scale_a,
+                                     int64_t scale_a_numel, const float* scale_b, int64_t scale_b_numel, void* out,
+                                     int64_t ldo, int64_t M, int64_t N, int64_t K, void* stream) {
+  if (M < 0 || N < 0 || K < 0 || N % 16 != 0) return FR_EINVAL;
+  // the MFMA kernel's operand conditions (there is no scalar SiLU variant)
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  if (M > 0 && N > 0 &&
+      (K == 0 || K % 16 != 0 || lda % 16 != 0 || ldb % 16 != 0 || !al16(a) || !al16(b) ||
+       (M - 1) * lda + K >= (int64_t(1) << 31) || (N - 1) * ldb + K >= (int64_t(1) << 31)))
+    return FR_EUNSUPPORTED;
+  return gemm_entry(a, lda, b, ldb, scale_a, scale_a_numel, scale_b, scale_b_numel, nullptr, 0, nullptr, 0, out, ldo,
+                    M, N, K, FR_DTYPE_BF16, stream, true);
 }

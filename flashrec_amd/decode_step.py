@@ -26,6 +26,7 @@ import torch
 
 from flashrec_amd.attention.paged import AttentionBackend
 from flashrec_amd.kernel.qk_rope_kv import fused_qk_norm_rope_store_fp8
+from flashrec_amd.kernel.sglops import per_token_quant_fp8
 from flashrec_amd.kernel.silu_fp8 import silu_and_mul_per_token_quant_fp8
 from flashrec_amd.kvcache.pool import TokenToKVPool
 from flashrec_amd.layers.linear import Linear
@@ -159,6 +160,10 @@ class Qwen3FP8DecodeStep:
             raise ValueError("no lm_head weight (and embeddings are not tied)")
         self.weights = weights
         self.layers = weights.layers
+        # gate_up weights with gate/up rows interleaved for the SiLU-and-mul
+        # epilogue, built once here rather than inside a captured step
+        for L in self.layers:
+            L.gate_up_proj._glu_operands()
         self.final_norm = weights.final_norm
         self.embed = weights.lm_head_weight
         self.rotary = RotaryEmbedding(shape.head_dim, shape.max_position, shape.rope_theta, device=dev)
@@ -275,7 +280,8 @@ class Qwen3FP8DecodeStep:
     def _layer_folded(self, L: _Layer, x: Optional[torch.Tensor], residual: Optional[torch.Tensor]):
         """The same layer with each residual add folded into the GEMM that
         produces the addend (o_proj, down_proj: fr_fp8_scaled_mm_residual),
-        so both RMSNorms run without their add: bit-for-bit ``_layer``, whose
+        so both RMSNorms run without their add, and SiLU-and-mul folded into
+        the gate_up GEMM (fr_fp8_scaled_mm_silu): bit-for-bit ``_layer``, whose
         fused add + RMSNorm rounds the GEMM output and then the sum the same
         way.  Takes and returns (None, residual) once the stream holds the
         sum; the first layer starts from (x, None) as ``_layer`` does."""
@@ -284,9 +290,11 @@ class Qwen3FP8DecodeStep:
         q_fp8, a_scale = L.input_layernorm.quant_fp8(residual)
         residual = self._attention(L, q_fp8, a_scale, residual)
         q_fp8, a_scale = L.post_attention_layernorm.quant_fp8(residual)
-        t = int(q_fp8.shape[0])
-        gu = L.gate_up_proj.forward_fp8(q_fp8, a_scale, (t, self.shape.hidden), torch.bfloat16)
-        y_fp8, y_scale = silu_and_mul_per_token_quant_fp8(gu)
+        # SiLU-and-mul in the gate_up GEMM's epilogue (half-width bf16 rows),
+        # then the per-token quant: bit-for-bit silu_and_mul_per_token_quant_fp8
+        # of the full gate_up output
+        h = L.gate_up_proj.forward_fp8_silu(q_fp8, a_scale)
+        y_fp8, y_scale = per_token_quant_fp8(h)
         residual = L.down_proj.forward_fp8_residual(y_fp8, y_scale, residual)
         return None, residual
 

@@ -224,6 +224,65 @@ def fp8_scaled_mm_residual(
     return out
 
 
+def interleave_gate_up(t: torch.Tensor, dim: int = 0) -> torch.Tensor:
+    """The gate half then the up half of ``t`` along ``dim`` (2n entries, n a
+    multiple of 8) reordered into chunks of 16: 8 gate entries followed by
+    the 8 up entries of the same output columns, the order
+    ``fp8_scaled_mm_silu`` takes its weight rows and scales in.  A copy."""
+    size = int(t.shape[dim])
+    if size % 16:
+        raise ValueError(f"gate/up interleave needs a multiple of 16 rows, got {size}")
+    shape = list(t.shape)
+    split = shape[:dim] + [2, size // 16, 8] + shape[dim + 1:]
+    return t.reshape(split).transpose(dim, dim + 1).reshape(shape).contiguous()
+
+
+@torch.compiler.disable
+def fp8_scaled_mm_silu(
+    a_fp8: torch.Tensor,
+    b_fp8: torch.Tensor,
+    scale_a: torch.Tensor,
+    scale_b: torch.Tensor,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """``silu_and_mul(fp8_scaled_mm(a, b, scale_a, scale_b, bf16))`` in one
+    GEMM, for weights whose gate/up columns were put in the order of
+    ``interleave_gate_up`` (``b`` ``[K, N]`` column-major and ``scale_b`` both
+    interleaved).  Bit-for-bit the two steps on the un-interleaved weights
+    (sglops.py:99-151): the product rounded to bf16, torch's silu in fp32
+    rounded to bf16, the product with up rounded to bf16.  Returns (or writes
+    into ``out``) ``[M, N / 2]`` bf16."""
+    if a_fp8.dtype != torch.float8_e4m3fn or b_fp8.dtype != torch.float8_e4m3fn:
+        raise TypeError("fp8_scaled_mm_silu takes float8_e4m3fn operands")
+    if a_fp8.dim() != 2 or b_fp8.dim() != 2 or a_fp8.shape[1] != b_fp8.shape[0]:
+        raise ValueError(f"shape mismatch: a {tuple(a_fp8.shape)} b {tuple(b_fp8.shape)}")
+    m, k = int(a_fp8.shape[0]), int(a_fp8.shape[1])
+    n = int(b_fp8.shape[1])
+    if n % 16:
+        raise ValueError(f"fp8_scaled_mm_silu needs N a multiple of 16, got {n}")
+    require_device(a_fp8, b_fp8)
+    if out is None:
+        out = torch.empty((m, n // 2), dtype=torch.bfloat16, device=a_fp8.device)
+    elif out.dtype != torch.bfloat16 or tuple(out.shape) != (m, n // 2) or out.stride(1) != 1:
+        raise ValueError(f"out must be [{m}, {n // 2}] bf16 with a unit inner stride")
+    require_device(out)
+    a = a_fp8 if a_fp8.stride(1) == 1 and (m <= 1 or a_fp8.stride(0) >= k) else a_fp8.contiguous()
+    b = b_fp8
+    if not (b.stride(0) == 1 and (n <= 1 or b.stride(1) >= k)):
+        b = b.t().contiguous().t()
+    a, b, k = _mfma_operands(a, b, m, n, k)
+    sa = scale_a.reshape(-1).to(device=a.device, dtype=torch.float32).contiguous()
+    sb = scale_b.reshape(-1).to(device=a.device, dtype=torch.float32).contiguous()
+    if sa.numel() not in (1, m) or sb.numel() not in (1, n):
+        raise ValueError("scale_a must have 1 or M values and scale_b 1 or N values")
+    lda = a.stride(0) if m > 1 else k
+    ldb = b.stride(1) if n > 1 else k
+    ldo = out.stride(0) if m > 1 else n // 2
+    call("fr_fp8_scaled_mm_silu", a.data_ptr(), lda, b.data_ptr(), ldb, sa.data_ptr(), sa.numel(),
+         sb.data_ptr(), sb.numel(), out.data_ptr(), ldo, m, n, k, stream_of(a))
+    return out
+
+
 @torch.compiler.disable
 def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
     """SwiGLU: ``silu(x[..., :d]) * x[..., d:]`` with ``d = last_dim // 2`` (sglops.py:143-151)."""
@@ -365,6 +424,8 @@ __all__ = [
     "apply_rope_inplace",
     "per_token_quant_fp8",
     "fp8_scaled_mm",
+    "fp8_scaled_mm_silu",
+    "interleave_gate_up",
     "silu_and_mul",
     "apply_rope_and_store_kv",
     "store_kv_cache",

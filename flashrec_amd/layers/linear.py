@@ -34,7 +34,8 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from flashrec_amd._lib import DTYPE_CODE, call, require_device, stream_of
-from flashrec_amd.kernel.sglops import fp8_scaled_mm, fp8_scaled_mm_residual, per_token_quant_fp8
+from flashrec_amd.kernel.sglops import (fp8_scaled_mm, fp8_scaled_mm_residual, fp8_scaled_mm_silu,
+                                        interleave_gate_up, per_token_quant_fp8)
 
 _E4M3 = torch.float8_e4m3fn
 _FP8_DTYPES = frozenset({torch.float8_e4m3fn, torch.float8_e5m2})
@@ -105,6 +106,16 @@ class Linear(nn.Module):
     def _fp8_scale(self) -> Optional[torch.Tensor]:
         return self.w_scale
 
+    def _glu_operands(self):
+        """The codes and scales with gate/up rows interleaved for
+        ``forward_fp8_silu``: built on first use (a copy of the codes, kept
+        until the weights change or move)."""
+        cached = self.__dict__.get("_glu")
+        if cached is None or cached[0].device != self.w_codes.device:
+            cached = (interleave_gate_up(self.w_codes), interleave_gate_up(self.w_scale))
+            self.__dict__["_glu"] = cached
+        return cached
+
     def _apply(self, fn, recurse=True):
         # Module.to() / .cuda() / .half() move the codes and scales to the new
         # device but never cast them: a float cast would destroy the e4m3 codes
@@ -152,6 +163,7 @@ class Linear(nn.Module):
 
     def _set_codes(self, codes: torch.Tensor, scale: torch.Tensor) -> None:
         # ``codes`` is the [N, K] matrix (a transposed [K, N] view stays a view)
+        self.__dict__.pop("_glu", None)
         self.w_codes = codes
         self.w_scale = scale.to(device=codes.device, dtype=torch.float32).reshape(self.out_features)
         self.weight = nn.Parameter(torch.empty(0, device=codes.device), requires_grad=False)
@@ -196,3 +208,19 @@ class Linear(nn.Module):
             raise ValueError(f"activations on {q.device}, fp8 weights on {self.w_codes.device}: "
                              "move the module with .to() first")
         return fp8_scaled_mm_residual(q, self.w_codes.t(), a_scale, self.w_scale, residual)
+
+    def forward_fp8_silu(self, q: torch.Tensor, a_scale: torch.Tensor, out: Optional[torch.Tensor] = None
+                         ) -> torch.Tensor:
+        """``silu_and_mul(forward_fp8(q, a_scale, ..., bf16))`` for a gate_up
+        projection (gate rows, then up rows) with SiLU-and-mul in the GEMM's
+        epilogue: ``[M, out_features / 2]`` bf16, bit-for-bit the two steps
+        (qwen3.py:144-172 up to the per-token quant).  No bias."""
+        if self.w_codes is None:
+            raise RuntimeError("Linear.forward_fp8_silu needs fp8 weights")
+        if self.bias is not None:
+            raise ValueError("forward_fp8_silu takes a Linear without bias")
+        if self.w_codes.device != q.device:
+            raise ValueError(f"activations on {q.device}, fp8 weights on {self.w_codes.device}: "
+                             "move the module with .to() first")
+        codes, scale = self._glu_operands()
+        return fp8_scaled_mm_silu(q, codes.t(), a_scale, scale, out)

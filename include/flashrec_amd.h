@@ -109,6 +109,23 @@ int fr_fp8_scaled_mm_residual(const void* a, int64_t lda, const void* b, int64_t
                               const void* residual, int64_t ldr, void* out, int64_t ldo, int64_t M, int64_t N,
                               int64_t K, int out_dtype, void* stream);
 
+/* fr_fp8_scaled_mm with SiLU-and-mul in its epilogue (bf16 only): the N
+ * weight rows of b come in chunks of 16, the 8 gate rows of a chunk followed
+ * by the 8 up rows of the same output columns; with p the bf16-rounded
+ * scaled product, out[m, 8k + c] = bf16(bf16(silu(p[m, 16k + c])) *
+ * p[m, 16k + 8 + c]) for c < 8, out [M, N / 2] bf16 with row stride ldo.
+ * N must be a multiple of 16.  Bit-for-bit fr_fp8_scaled_mm followed by
+ * fr_silu_and_mul on the de-interleaved product (torch's silu in fp32, the
+ * bf16 rounding after silu and after the product).  Replaces, in the MLP
+ * (python/flashrec/models/qwen3.py:144-172), gate_up_proj followed by the
+ * SiLU-and-mul half of silu_and_mul_per_token_quant_fp8
+ * (python/flashrec/kernel/silu_fp8.py:79-82): the per-token quant of out
+ * (fr_per_token_quant_fp8) completes that call.  Operands the MFMA kernel
+ * cannot take (K % 16, unaligned rows) give FR_EUNSUPPORTED. */
+int fr_fp8_scaled_mm_silu(const void* a, int64_t lda, const void* b, int64_t ldb, const float* scale_a,
+                          int64_t scale_a_numel, const float* scale_b, int64_t scale_b_numel, void* out,
+                          int64_t ldo, int64_t M, int64_t N, int64_t K, void* stream);
+
 /* Per-head RMSNorm of q and k (weights q_weight, k_weight: bf16 [D]),
  * NeoX rotate-half RoPE from cos_sin_cache ([cache_rows, D] fp32: cos for
  * i < D/2, sin after), q rotated in place (bf16), rotated k and raw v

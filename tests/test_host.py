@@ -98,6 +98,33 @@ def test_scaled_mm_abi_rejects_bias_length():
     assert rc == _lib.FR_EINVAL
 
 
+def test_silu_gemm_abi_rejects_bad_shapes():
+    """fr_fp8_scaled_mm_silu: N not a multiple of 16 is FR_EINVAL, K not a
+    multiple of 16 FR_EUNSUPPORTED (no scalar SiLU kernel), both before any launch."""
+    from flashrec_amd import _lib
+
+    lib = _lib.load()
+    p = 4096
+    assert lib.fr_fp8_scaled_mm_silu(p, 256, p, 256, p, 64, p, 248, p, 128, 64, 248, 256, None) == _lib.FR_EINVAL
+    assert lib.fr_fp8_scaled_mm_silu(p, 256, p, 256, p, 64, p, 256, p, 128, 64, 256, 250, None) == \
+        _lib.FR_EUNSUPPORTED
+
+
+def test_interleave_gate_up_order():
+    """Chunks of 16: 8 gate rows, then the 8 up rows of the same columns."""
+    from flashrec_amd.kernel.sglops import interleave_gate_up
+
+    n = 24
+    w = torch.arange(2 * n * 3).reshape(2 * n, 3)
+    got = interleave_gate_up(w)
+    want = [r for c in range(n // 8) for r in list(range(8 * c, 8 * c + 8)) + list(range(n + 8 * c, n + 8 * c + 8))]
+    assert torch.equal(got, w[want])
+    assert torch.equal(interleave_gate_up(torch.arange(2 * n)), torch.arange(2 * n)[want])
+    assert torch.equal(interleave_gate_up(w.t().contiguous(), dim=1), w[want].t())
+    with pytest.raises(ValueError):
+        interleave_gate_up(torch.zeros(40, 2))
+
+
 def test_log_softmax_rejects_mismatched_out():
     from flashrec_amd.kernel.sglops import log_softmax_f32
 
