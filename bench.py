@@ -77,8 +77,11 @@ def _copies(nbytes: int) -> int:
     return max(2, math.ceil(MALL_DEFEAT_BYTES / max(1, nbytes)))
 
 
-def _gemm_case(dev, m, n, k, steps, warmup, seed, rotate=True):
-    from flashrec_amd.kernel.sglops import fp8_scaled_mm, per_token_quant_fp8
+def _gemm_case(dev, m, n, k, steps, warmup, seed, rotate=True, silu=False):
+    """W8A8 GEMM TFLOP/s over rotated operands; ``silu``: the SiLU-and-mul
+    epilogue variant (half-width bf16 output; random weights, so their
+    gate/up order does not matter)."""
+    from flashrec_amd.kernel.sglops import fp8_scaled_mm, fp8_scaled_mm_silu, per_token_quant_fp8
     from flashrec_amd.layers.linear import quantize_weight_fp8
 
     g = torch.Generator(device=dev).manual_seed(seed)
@@ -91,17 +94,52 @@ def _gemm_case(dev, m, n, k, steps, warmup, seed, rotate=True):
         q, s = quantize_weight_fp8(w)
         weights.append((q.t(), s))
         del x, w
-    out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+    out = torch.empty(m, n // 2 if silu else n, dtype=torch.bfloat16, device=dev)
 
     def step(i):
         qa, sa = acts[i % reps]
         qw, sw = weights[i % reps]
-        fp8_scaled_mm(qa, qw, sa, sw, torch.bfloat16)
+        if silu:
+            fp8_scaled_mm_silu(qa, qw, sa, sw, out)
+        else:
+            fp8_scaled_mm(qa, qw, sa, sw, torch.bfloat16)
 
     ms = _timed(step, steps, warmup)
     del acts, weights, out
     flops = 2.0 * m * n * k
     return ms, flops / (ms * 1e-3) / 1e12
+
+
+def _vendor_gemm_case(dev, m, n, k, steps, warmup, seed, rowwise=True):
+    """The vendor library on the same shape, for comparison only: torch._scaled_mm
+    (hipBLASLt on ROCm) with e4m3 operands rotated as in _gemm_case, per-row /
+    per-column scales (``rowwise``, the path's own scaling) or one scale per
+    tensor.  Returns (ms, TFLOP/s), or None when the build refuses the call."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    reps = _copies(m * k + n * k)
+    ops = []
+    for _ in range(reps):
+        a = torch.randn(m, k, device=dev, generator=g).to(torch.float8_e4m3fn)
+        b = (0.02 * torch.randn(n, k, device=dev, generator=g)).to(torch.float8_e4m3fn).t()
+        if rowwise:
+            sa = torch.rand(m, 1, device=dev, generator=g) + 0.5
+            sb = torch.rand(1, n, device=dev, generator=g) + 0.5
+        else:
+            sa = torch.tensor(1.0, device=dev)
+            sb = torch.tensor(1.0, device=dev)
+        ops.append((a, b, sa, sb))
+
+    def step(i):
+        a, b, sa, sb = ops[i % reps]
+        torch._scaled_mm(a, b, scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16)
+
+    try:
+        step(0)
+    except (RuntimeError, NotImplementedError):
+        return None
+    ms = _timed(step, steps, warmup)
+    del ops
+    return ms, 2.0 * m * n * k / (ms * 1e-3) / 1e12
 
 
 def _decode_step_case(dev):
@@ -490,6 +528,20 @@ def main() -> int:
         ms1, tf1 = _gemm_case(dev, 512, 12288, 2048, steps, warm, seed=11)
         extra["config1_gemm_M512"] = {"ms": round(ms1, 5), "TFLOP/s": round(tf1, 2),
                                       "frac": round(tf1 / PEAK_FP8_TFLOPS, 4)}
+        for name, rw in (("vendor_hipblaslt_config1_rowwise", True), ("vendor_hipblaslt_config1_tensorwise", False)):
+            vend = _vendor_gemm_case(dev, 4096, 12288, 2048, steps, warm, seed=7, rowwise=rw)
+            if vend is not None:
+                extra[name] = {"ms": round(vend[0], 5), "TFLOP/s": round(vend[1], 2),
+                               "frac": round(vend[1] / PEAK_FP8_TFLOPS, 4),
+                               "what": "torch._scaled_mm (hipBLASLt) on the headline shape, same operand "
+                                       "rotation; for comparison, not this library"}
+        msb, tfb = _gemm_case(dev, 8192, 8192, 8192, steps, warm, seed=9)
+        extra["gemm_8192_cube"] = {"ms": round(msb, 5), "TFLOP/s": round(tfb, 2),
+                                   "frac": round(tfb / PEAK_FP8_TFLOPS, 4)}
+        mss, tfs = _gemm_case(dev, 4096, 12288, 2048, steps, warm, seed=3, silu=True)
+        extra["config1_gate_up_silu_gemm"] = {
+            "ms": round(mss, 5), "TFLOP/s": round(tfs, 2), "frac": round(tfs / PEAK_FP8_TFLOPS, 4),
+            "what": "the headline GEMM with SiLU-and-mul in its epilogue (the decode step's gate_up)"}
         ms2, tf2 = _gemm_case(dev, 4096, 2048, 6144, steps, warm, seed=2)
         extra["config2_down_gemm"] = {"ms": round(ms2, 5), "TFLOP/s": round(tf2, 2),
                                       "frac": round(tf2 / PEAK_FP8_TFLOPS, 4)}
