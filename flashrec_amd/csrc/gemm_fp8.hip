@@ -1034,19 +1034,22 @@ static hipError_t dispatch(const GemmArgs& g, hipStream_t st) {
   }
   // Tile choice: the shape with the least estimated time, rounds of tiles
   // over the CUs (persistent workgroups: a partial round costs a full one)
-  // times a tile's MFMA work over its relative K-loop efficiency.  The
-  // efficiencies are measured TFLOP/s per tile shape on 4096-row shapes
-  // (256x256 1.0, 256x128 0.9, 192x128 0.85, 128x128 0.7).  E.g. M=4096,
-  // N=12288 takes 256x256 (3 rounds); N=2048 takes 256x128 (one round);
-  // M=512, N=12288 takes 192x128 (256 tiles: one round on every CU, where
-  // 256x128 leaves 64 CUs idle).
+  // times a tile's MFMA work over its relative efficiency (256x256 1.0,
+  // 256x128 0.75, 192x128 0.72, 128x128 0.6), fitted so that the choice is
+  // the fastest of the four, timed with every tile forced, on the config
+  // shapes and on M = 768..3072 x N = 12288, M = 1024 x N = 4096 and
+  // M = 2048 x N = 2048 (K = 2048 or 6144).  E.g. M=4096, N=12288 takes
+  // 256x256 (3 rounds); N=2048 takes 256x128 (one round); M=512, N=12288
+  // takes 192x128 (256 tiles: one round on every CU, where 256x128 leaves 64
+  // CUs idle); M=1024..3072, N=12288 take 256x256 (3-10 % over the smaller
+  // tiles' extra rounds).
   const int64_t cus = num_cus();
   auto tiles = [&](int bn, int bm) __attribute__((always_inline)) { return ((g.N + bn - 1) / bn) * ((g.M + bm - 1) / bm); };
   auto cost = [&](int bn, int bm, double eff) __attribute__((always_inline)) {
     return static_cast<double>((tiles(bn, bm) + cus - 1) / cus) * bn * bm / eff;
   };
-  const double c256 = cost(256, 256, 1.0), c2561 = cost(256, 128, 0.9), c192 = cost(192, 128, 0.85),
-               c128 = cost(128, 128, 0.7);
+  const double c256 = cost(256, 256, 1.0), c2561 = cost(256, 128, 0.75), c192 = cost(192, 128, 0.72),
+               c128 = cost(128, 128, 0.6);
   // the residual add and SiLU-and-mul are variants of their own, so the
   // plain kernels carry none of their code (measured 1-3 % on every tile
   // shape when the residual was a runtime branch); only 16-bit outputs take
