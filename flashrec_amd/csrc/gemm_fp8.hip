@@ -615,7 +615,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
       if constexpr (SILU) {
         // 8-column groups 2k (gate) and 2k + 1 (up) of the pass are one chunk
         float gt[NQO][4], up[NQO][4], sg[NQO][4];
-        bool wide = false;
+        float gmax = 0.0f;  // max |gate| (NaN-propagating)
 #pragma unroll
         for (int k = 0; k < NQO; ++k) {
           const int col = cg * CPP + 16 * k;
@@ -632,12 +632,12 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_mfma(GemmArgs g) {
           }
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            wide = wide || !(__builtin_fabsf(gt[k][e]) <= 80.0f);
+            gmax = maxnan(gmax, __builtin_fabsf(gt[k][e]));
             sg[k][e] = silu_in_range(gt[k][e]);
           }
         }
         // gates beyond the in-range form (|g| > 80, inf, NaN): torch's formula
-        if (__builtin_expect(__ballot(wide) != 0, 0)) {
+        if (__builtin_expect(__ballot(!(gmax <= 80.0f)) != 0, 0)) {
 #pragma unroll
           for (int k = 0; k < NQO; ++k)
 #pragma unroll
