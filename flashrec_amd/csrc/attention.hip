@@ -325,7 +325,9 @@ __device__ __forceinline__ bf16x8_t e4m3x8_to_bf16(uint32_t w0, uint32_t w1) {
   const bf16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true);
   const bf16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false);
   const bf16x2_t d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true);
-  return bf16x8_t{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+  // each pair is one dword: the vector is the four dwords as they are
+  return __builtin_bit_cast(bf16x8_t, u32x4{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                                            __builtin_bit_cast(uint32_t, c), __builtin_bit_cast(uint32_t, d)});
 }
 
 constexpr int kVRow = 288;  // LDS bytes per staged V row: 256 + 32 (bank spread)
@@ -430,11 +432,15 @@ __device__ __forceinline__ void grouped_item(const AttnArgs& a, uint8_t* vs, int
   auto compute = [&](int32_t bi, Loaded& L, auto own_c) __attribute__((always_inline)) {
     constexpr bool OWN = decltype(own_c)::value;
     const int32_t pos_base = P32 + (bi - nshared) * NREP;
-    const uint64_t rows_ok = __ballot(L.ok);  // bit r (r < 32): key row r usable
+    // bit r: key row r usable (lanes 32-63 load the same rows as 0-31)
+    const uint32_t rows_ok = static_cast<uint32_t>(__ballot(L.ok));
+    const bool all_rows = rows_ok == 0xFFFFFFFFu;
+    if (!all_rows) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int w = 0; w < 4; ++w) L.vw[i][w] = L.ok ? L.vw[i][w] : 0u;
+        for (int w = 0; w < 4; ++w) L.vw[i][w] = L.ok ? L.vw[i][w] : 0u;
+    }
     // S^T = K . Q^T
     f32x16_t S;
 #pragma unroll
@@ -452,25 +458,26 @@ __device__ __forceinline__ void grouped_item(const AttnArgs& a, uint8_t* vs, int
       *reinterpret_cast<bf16x8_t*>(vs + n * kVRow + 128 * h + 32 * i) = lo;
       *reinterpret_cast<bf16x8_t*>(vs + n * kVRow + 128 * h + 32 * i + 16) = hi;
     }
-    // scores of this lane's query against key rows r = 8(v/4) + 4h + v%4
+    // scores of this lane's query against key rows r = 8(v/4) + 4h + v%4,
+    // unscaled (the scale is positive: the block max scales with them, and
+    // each probability takes the scale in one fma)
     float x[16];
-    const bool all_rows = static_cast<uint32_t>(rows_ok) == 0xFFFFFFFFu;
     if (!OWN && all_rows) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) x[v] = S[v] * a.qscale;
+      for (int v = 0; v < 16; ++v) x[v] = S[v];
     } else {
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int r = 8 * (v / 4) + 4 * h + (v % 4);
-        bool ok = (rows_ok >> r) & 1;
+        bool ok = (rows_ok >> r) & 1u;
         if (OWN) ok = ok && (r / NREP == n / NREP) && (pos_base + r % NREP < qlen);
-        x[v] = ok ? S[v] * a.qscale : -__builtin_inff();
+        x[v] = ok ? S[v] : -__builtin_inff();
       }
     }
     float mb = x[0];
 #pragma unroll
     for (int v = 1; v < 16; ++v) mb = __builtin_fmaxf(mb, x[v]);
-    mb = __builtin_fmaxf(mb, __shfl_xor(mb, 32, 64));
+    mb = __builtin_fmaxf(mb, __shfl_xor(mb, 32, 64)) * a.qscale;
     // Lazy rescale: probabilities are taken against the reference max m and
     // may reach 2^8; the accumulators are rescaled only when some query's
     // block max passes m + 8 (wave-uniform, so O is touched rarely).
@@ -491,18 +498,17 @@ __device__ __forceinline__ void grouped_item(const AttnArgs& a, uint8_t* vs, int
     float pr[16];
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      pr[v] = __builtin_amdgcn_exp2f(x[v] - mref);  // x = -inf gives 0
+      pr[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[v], a.qscale, -mref));  // x = -inf gives 0
       l += pr[v];
     }
     bf16x8_t pb[2];
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
+    for (int c = 0; c < 2; ++c) {
+      u32x4 w;
 #pragma unroll
-      for (int t = 0; t < 8; t += 2) {
-        const uint32_t w = pack_bf16x2(pr[8 * c + t], pr[8 * c + t + 1]);
-        pb[c][t] = __builtin_bit_cast(__bf16, static_cast<uint16_t>(w & 0xFFFFu));
-        pb[c][t + 1] = __builtin_bit_cast(__bf16, static_cast<uint16_t>(w >> 16));
-      }
+      for (int t = 0; t < 4; ++t) w[t] = pack_bf16x2(pr[8 * c + 2 * t], pr[8 * c + 2 * t + 1]);
+      pb[c] = __builtin_bit_cast(bf16x8_t, w);
+    }
     // O^T += V^T . P^T; A[dim][k] through the transposing LDS read
     const int g = lane >> 4, i16 = lane & 15;
 #pragma unroll
