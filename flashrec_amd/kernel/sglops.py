@@ -266,6 +266,8 @@ def fp8_scaled_mm_silu(
     elif out.dtype != torch.bfloat16 or tuple(out.shape) != (m, n // 2) or out.stride(1) != 1:
         raise ValueError(f"out must be [{m}, {n // 2}] bf16 with a unit inner stride")
     require_device(out)
+    if k == 0:  # an empty product: silu(0) * 0
+        return out.zero_()
     a = a_fp8 if a_fp8.stride(1) == 1 and (m <= 1 or a_fp8.stride(0) >= k) else a_fp8.contiguous()
     b = b_fp8
     if not (b.stride(0) == 1 and (n <= 1 or b.stride(1) >= k)):
