@@ -487,7 +487,7 @@ def main() -> int:
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
-              "(the FP8 path is single-GPU; see the sharding note in DESIGN.md)", file=sys.stderr)
+              "(the FP8 path is measured on one GPU: its kernels shard by beam rows, one KV pool per GPU)", file=sys.stderr)
         return 2
     from flashrec_amd._lib import load
 
