@@ -110,6 +110,20 @@ def test_silu_gemm_abi_rejects_bad_shapes():
         _lib.FR_EUNSUPPORTED
 
 
+def test_silu_gemm_wrapper_checks_before_the_device():
+    """fp8_scaled_mm_silu refuses wrong dtypes, mismatched K and N not a multiple of 16 before any launch."""
+    from flashrec_amd.kernel.sglops import fp8_scaled_mm_silu
+
+    a = torch.zeros(4, 32, dtype=torch.float8_e4m3fn)
+    b = torch.zeros(40, 32, dtype=torch.float8_e4m3fn).t()
+    with pytest.raises(ValueError, match="multiple of 16"):
+        fp8_scaled_mm_silu(a, b, torch.ones(4, 1), torch.ones(40))
+    with pytest.raises(TypeError):
+        fp8_scaled_mm_silu(a.float(), b, torch.ones(4, 1), torch.ones(40))
+    with pytest.raises(ValueError, match="shape mismatch"):
+        fp8_scaled_mm_silu(a, torch.zeros(32, 16, dtype=torch.float8_e4m3fn), torch.ones(4, 1), torch.ones(32))
+
+
 def test_interleave_gate_up_order():
     """Chunks of 16: 8 gate rows, then the 8 up rows of the same columns."""
     from flashrec_amd.kernel.sglops import interleave_gate_up
