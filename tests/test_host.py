@@ -121,7 +121,7 @@ def test_silu_gemm_wrapper_checks_before_the_device():
     with pytest.raises(TypeError):
         fp8_scaled_mm_silu(a.float(), b, torch.ones(4, 1), torch.ones(40))
     with pytest.raises(ValueError, match="shape mismatch"):
-        fp8_scaled_mm_silu(a, torch.zeros(32, 16, dtype=torch.float8_e4m3fn), torch.ones(4, 1), torch.ones(32))
+        fp8_scaled_mm_silu(a, torch.zeros(48, 16, dtype=torch.float8_e4m3fn), torch.ones(4, 1), torch.ones(16))
 
 
 def test_interleave_gate_up_order():
