@@ -206,9 +206,12 @@ def test_gemm_config4_shapes_all_rows(dev, name, n, k):
 
 
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32, torch.float16])
-@pytest.mark.parametrize("m,n,k", [(4096 + 100, 12288, 2048), (4096, 2048 + 64, 6144)])
+@pytest.mark.parametrize("m,n,k", [(4096 + 100, 12288, 2048), (2661, 6144, 2048), (1381, 12352, 2048),
+                                   (3685, 2176, 2048)])
 def test_gemm_multi_tile_edges(dev, m, n, k, out_dtype):
-    """Several tiles per workgroup with edge tiles among them: after a
+    """Several tiles per workgroup with edge tiles among them, on each tile
+    shape (the tile choice gives these 256x256 in 4 rounds, 256x128 in 2,
+    192x128 in 3 with a partial last column tile, 128x128 in 2): after a
     partial tile's epilogue the next tile's first waits must not assume the
     full tile's store count (and after a full one they may).  Seeded rows,
     including every row of the last (partial) m-tile, against the oracle."""
@@ -222,12 +225,14 @@ def test_gemm_multi_tile_edges(dev, m, n, k, out_dtype):
     assert torch.isfinite(out).all()
 
 
-@pytest.mark.parametrize("m,n,k", [(2048 + 37, 4096, 2064), (4096, 2048, 1088), (512, 12288, 2112)])
+@pytest.mark.parametrize("m,n,k", [(1637, 12288, 2064), (2624, 6144, 1088), (1344, 12288, 2112),
+                                   (3648, 2112, 1040), (4096, 2048, 1088), (512, 12288, 2112)])
 def test_gemm_k_tail_multi_tile(dev, m, n, k):
-    """K not a multiple of the 128-byte ring rows (K % 128 = 16, 64, 64) on
-    shapes that give workgroups several tiles (256x256, 256x128 and the
-    single-round 256x128 path): the zero-filled tail of each tile's last slot
-    must not leak into the next tile's first slots."""
+    """K not a multiple of the 128-byte ring rows (K % 128 = 16, 64, 64, 16)
+    on shapes that give workgroups several tiles of each shape (256x256 in 2
+    rounds, 256x128 in 2, 192x128 in 3, 128x128 in 2) and on two one-round
+    shapes: the zero-filled tail of each tile's last slot must not leak into
+    the next tile's first slots."""
     qa, sa, qw, sw = _operands(m, n, k, seed=k)
     out = _run(dev, qa, sa, qw, sw).cpu()
     g = torch.Generator().manual_seed(6)

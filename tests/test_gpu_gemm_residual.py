@@ -8,7 +8,9 @@ rounds the fp32 sum once: the reference's ``residual + x``,
 sglops.py:53-55).  Covered: the decode step's o and down shapes (the
 256 x 128 tile's fast epilogue), edge tiles and tails (the bounds-checked
 path), the 256 x 256 tile (which routes the add through the bounds-checked
-path), fp16, in place and into a separate buffer, a strided residual."""
+path), the 192 x 128 and 128 x 128 tiles and several tiles per workgroup
+(M = 512, 1381 and 2661 rows), fp16, in place and into a separate buffer, a
+strided residual."""
 
 import pytest
 import torch
@@ -50,7 +52,8 @@ def _assert_same(got, ref, label=""):
 
 
 @pytest.mark.parametrize("m,n,k", [(4096, 2048, 2048), (4096, 2048, 6144), (300, 520, 384), (33, 100, 256),
-                                   (4096 + 100, 2048 + 64, 2048), (512, 2048, 1040), (1, 256, 2048)])
+                                   (4096 + 100, 2048 + 64, 2048), (512, 2048, 1040), (1, 256, 2048),
+                                   (512, 12288, 2048), (1381, 12352, 2048), (2661, 6144, 2048)])
 def test_residual_in_place_matches_two_steps(dev, m, n, k):
     from flashrec_amd.kernel.sglops import fp8_scaled_mm_residual
 

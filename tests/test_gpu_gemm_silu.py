@@ -14,8 +14,9 @@ Bars:
   silu_and_mul_per_token_quant_fp8 of the GPU's gate_up output, at the fp8
   parity bar.
 Shapes: the decode step's gate_up (256 x 256 tile), M = 512 (256 x 128),
-small N (128 x 128), ragged M and N (the bounds-checked path), M = 1, and
-K not a multiple of 16 (operands repacked by the wrapper)."""
+small N (128 x 128), ragged M and N (the bounds-checked path), M = 1, K not
+a multiple of 16 (operands repacked by the wrapper), and several tiles per
+workgroup on the 256 x 128 and 128 x 128 tiles."""
 
 import pytest
 import torch
@@ -62,7 +63,7 @@ def _assert_same(got, ref, label=""):
 
 @pytest.mark.parametrize("m,n,k", [(4096, 12288, 2048), (512, 12288, 2048), (256, 2048, 1024),
                                    (300, 1040, 384), (4096 + 100, 2048 + 64, 2048), (33, 96, 256),
-                                   (1, 256, 2048), (64, 512, 1000)])
+                                   (1, 256, 2048), (64, 512, 1000), (2624, 6144, 2048), (3648, 2112, 1024)])
 def test_silu_epilogue_matches_two_steps(dev, m, n, k):
     from flashrec_amd.kernel.sglops import silu_and_mul
 
