@@ -55,7 +55,7 @@ __global__ __launch_bounds__(256) void log_softmax_rows_block(const float* x, in
   const f32x4* xr = reinterpret_cast<const f32x4*>(x + row * ldx);
   f32x4 v[NCH];
 #pragma unroll
-  for (int j = 0; j < NCH; ++j) v[j] = ldnt(xr + t + 256 * j);
+  for (int j = 0; j < NCH; ++j) v[j] = ldkeep(xr + t + 256 * j);
   // max; a NaN anywhere makes the row NaN below (x - max is NaN for it, and
   // the sum of exp with it)
   float m = -__builtin_inff();

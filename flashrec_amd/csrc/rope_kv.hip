@@ -118,7 +118,7 @@ __global__ __launch_bounds__(256) void qk_rope_kv_d128(RopeArgs a) {
 
   u32x4 xv[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) xv[r] = ldnt(reinterpret_cast<const u32x4*>(src + 4 * r * hstride + e0));
+  for (int r = 0; r < R; ++r) xv[r] = ldkeep(reinterpret_cast<const u32x4*>(src + 4 * r * hstride + e0));
   u32x4 wv;
   if (FUSED) wv = *reinterpret_cast<const u32x4*>(wp + e0);
   if (pos < 0 || pos >= a.cs_rows) return;  // no cache row: leave q / slot untouched

@@ -232,9 +232,9 @@ __global__ __launch_bounds__(256) void row_kernel_vec(RowArgs a) {
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       if (in(j)) {
-        xv[j] = ldnt(reinterpret_cast<const u32x4*>(xr + col(j)));
-        if (MODE == kSilu) uv[j] = ldnt(reinterpret_cast<const u32x4*>(xr + K + col(j)));
-        if (MODE == kAddRms) uv[j] = ldnt(reinterpret_cast<const u32x4*>(a.res + row * a.ldr + col(j)));
+        xv[j] = kNorm ? ldkeep(reinterpret_cast<const u32x4*>(xr + col(j)))
+                      : ldnt(reinterpret_cast<const u32x4*>(xr + col(j)));
+        if (MODE == kAddRms) uv[j] = ldkeep(reinterpret_cast<const u32x4*>(a.res + row * a.ldr + col(j)));
       } else {
         xv[j] = u32x4{0, 0, 0, 0};
         uv[j] = u32x4{0, 0, 0, 0};
@@ -339,9 +339,11 @@ __global__ __launch_bounds__(256) void row_kernel_split(RowArgs a) {
   u32x4 xv[NC], uv[NC], wv[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    xv[c] = in(c) ? ldnt(reinterpret_cast<const u32x4*>(xr + col(c))) : u32x4{0, 0, 0, 0};
+    xv[c] = !in(c) ? u32x4{0, 0, 0, 0}
+            : kNorm ? ldkeep(reinterpret_cast<const u32x4*>(xr + col(c)))
+                    : ldnt(reinterpret_cast<const u32x4*>(xr + col(c)));
     if (MODE == kAddRms)
-      uv[c] = in(c) ? ldnt(reinterpret_cast<const u32x4*>(a.res + row * a.ldr + col(c))) : u32x4{0, 0, 0, 0};
+      uv[c] = in(c) ? ldkeep(reinterpret_cast<const u32x4*>(a.res + row * a.ldr + col(c))) : u32x4{0, 0, 0, 0};
     if (kNorm) wv[c] = in(c) ? *reinterpret_cast<const u32x4*>(a.w + col(c)) : u32x4{0, 0, 0, 0};
   }
   float v[NC][8];
