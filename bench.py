@@ -180,6 +180,10 @@ def _decode_step_case(dev):
     ms_b = _graph_timed(lambda _i: m.beam_step(lp), 1)
     out["config4_beam_tail"] = {"ms": round(ms_b, 5), "rows": rows, "candidates_per_row": m.beam_cand,
                                 "select_k": m.beam_bw, "kernels": "row_topk + genrec (2 kernels)"}
+    ms_f = _graph_timed(lambda _i: m.beam_step(lp, from_logits=True), 1)
+    out["config4_beam_tail_from_logits"] = {
+        "ms": round(ms_f, 5), "what": "the same tail taking the head's logits, the log-softmax folded into "
+                                      "the row top-k (the decode step's form; replaces log_softmax + row_topk)"}
     p = m.attn._plan
     q = torch.randn(rows, shape.q_heads, shape.head_dim, device=dev).to(torch.bfloat16)
     o = torch.empty_like(q)

@@ -86,6 +86,7 @@ SIGNATURES = {
     "fr_trie_advance_nodes": [_P, _P, _P, _P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P],
     "fr_beam_expand_token_ids": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
     "fr_row_topk": [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P],
+    "fr_log_softmax_row_topk": [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P],
     "fr_paged_attention_fp8": [
         _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,  # q, k_cache, v_cache + strides
         _I64, _P, _P, _P,  # num_slots, kv_indices, kv_start, kv_len

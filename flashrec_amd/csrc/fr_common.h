@@ -255,6 +255,37 @@ __device__ __forceinline__ float row16_sum(float v) {
 // 16-byte vector type for coalesced loads/stores.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// log(sum(exp(x))) of one row held by a 256-thread workgroup, thread t owning
+// the float4 chunks t + 256 j (j < NCH): the row max (wave, then the four
+// wave maxima), the sum of exp(x - max) in a fixed order (per thread the
+// chunks in order, each as (e0 + e1) + (e2 + e3); the wave sum; then
+// (w0 + w1) + (w2 + w3)), and max + log(sum).  One definition for the
+// log-softmax kernel and the top-k that folds the log-softmax in, so the two
+// agree to the bit.  A NaN anywhere, or a row of -inf, gives NaN.  red: 8
+// floats of LDS; every thread of the workgroup must call it.
+template <int NCH>
+__device__ __forceinline__ float block_row_lse(const f32x4 (&v)[NCH], float* red) {
+  const int t = threadIdx.x;
+  const int lane = t & 63, w = t >> 6;
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int j = 0; j < NCH; ++j)
+    m = __builtin_fmaxf(__builtin_fmaxf(m, __builtin_fmaxf(v[j].x, v[j].y)), __builtin_fmaxf(v[j].z, v[j].w));
+  m = wave_max(m);
+  if (lane == 0) red[w] = m;
+  __syncthreads();
+  m = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) s += (expf(v[j].x - m) + expf(v[j].y - m)) + (expf(v[j].z - m) + expf(v[j].w - m));
+  s = wave_sum(s);
+  if (lane == 0) red[4 + w] = s;
+  __syncthreads();
+  s = (red[4] + red[5]) + (red[6] + red[7]);
+  return m + logf(s);
+}
 
 // ---------------------------------------------------------------- per-token quant
 // NaN-propagating max (v_maximum3_f32): torch's amax propagates NaN.

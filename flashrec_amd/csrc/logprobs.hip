@@ -49,31 +49,12 @@ __global__ __launch_bounds__(256) void log_softmax_rows_block(const float* x, in
                                                               int64_t ldo) {
   __shared__ float red[8];
   const int t = threadIdx.x;
-  const int lane = t & 63, w = t >> 6;
   const int64_t row = blockIdx.x;
-  typedef float f32x4 __attribute__((ext_vector_type(4)));
   const f32x4* xr = reinterpret_cast<const f32x4*>(x + row * ldx);
   f32x4 v[NCH];
 #pragma unroll
   for (int j = 0; j < NCH; ++j) v[j] = ldkeep(xr + t + 256 * j);
-  // max; a NaN anywhere makes the row NaN below (x - max is NaN for it, and
-  // the sum of exp with it)
-  float m = -__builtin_inff();
-#pragma unroll
-  for (int j = 0; j < NCH; ++j)
-    m = __builtin_fmaxf(__builtin_fmaxf(m, __builtin_fmaxf(v[j].x, v[j].y)), __builtin_fmaxf(v[j].z, v[j].w));
-  m = wave_max(m);
-  if (lane == 0) red[w] = m;
-  __syncthreads();
-  m = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
-  float s = 0.0f;
-#pragma unroll
-  for (int j = 0; j < NCH; ++j) s += (expf(v[j].x - m) + expf(v[j].y - m)) + (expf(v[j].z - m) + expf(v[j].w - m));
-  s = wave_sum(s);
-  if (lane == 0) red[4 + w] = s;
-  __syncthreads();
-  s = (red[4] + red[5]) + (red[6] + red[7]);
-  const float lse = m + logf(s);
+  const float lse = block_row_lse<NCH>(v, red);
   f32x4* orow = reinterpret_cast<f32x4*>(out + row * ldo);
 #pragma unroll
   for (int j = 0; j < NCH; ++j) stnt(orow + t + 256 * j, v[j] - lse);

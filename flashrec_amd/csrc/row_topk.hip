@@ -97,8 +97,12 @@ __device__ __forceinline__ uint32_t fresh_s(uint32_t v) {
   return v;
 }
 
-template <int NCH, int PT, bool FULL>
+// LSM: the scores are log_softmax(x) of the row, x - lse with lse from
+// block_row_lse (the log-softmax kernel's own arithmetic), formed in
+// registers and never written; FULL rows only.
+template <int NCH, int PT, bool FULL, bool LSM>
 __global__ __launch_bounds__(kThreads) void row_topk_kernel(TopkArgs a) {
+  static_assert(FULL || !LSM, "the folded log-softmax takes whole aligned rows");
   constexpr int NK = NCH * 4;
   constexpr int N = kThreads * PT;  // sort network width
   __shared__ uint32_t hist[kBins];
@@ -107,6 +111,7 @@ __global__ __launch_bounds__(kThreads) void row_topk_kernel(TopkArgs a) {
   __shared__ uint32_t sel[4];
   __shared__ uint64_t sk[N];
   __shared__ uint64_t cl[64];
+  __shared__ float lred[8];
 
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -119,8 +124,23 @@ __global__ __launch_bounds__(kThreads) void row_topk_kernel(TopkArgs a) {
 
   // ---- the row, as order-preserving bits; element q is index 4*(t + 256*(q/4)) + q%4
   uint32_t key[NK];
+  float lse = 0.0f;
+  if constexpr (LSM) {
+    fr::f32x4 v[NCH];
 #pragma unroll
-  for (int j = 0; j < NCH; ++j) {
+    for (int j = 0; j < NCH; ++j) v[j] = *reinterpret_cast<const fr::f32x4*>(xr + 4 * (t + kThreads * j));
+    lse = fr::block_row_lse<NCH>(v, lred);
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const fr::f32x4 y = v[j] - lse;
+      key[4 * j + 0] = score_bits(y.x);
+      key[4 * j + 1] = score_bits(y.y);
+      key[4 * j + 2] = score_bits(y.z);
+      key[4 * j + 3] = score_bits(y.w);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NCH && !LSM; ++j) {
     const int i0 = 4 * (t + kThreads * j);
     if (FULL || (a.vec && i0 + 3 < a.V)) {
       const float4 f = *reinterpret_cast<const float4*>(xr + i0);
@@ -349,7 +369,7 @@ __global__ __launch_bounds__(kThreads) void row_topk_kernel(TopkArgs a) {
     // that their bits come out as stored
     const uint32_t kb = static_cast<uint32_t>(kk >> 16);
     const float val = (kb == 0x80000000u || kb == 0xFFFFFFFFu)
-                          ? xr[idx]
+                          ? (LSM ? xr[idx] - lse : xr[idx])
                           : __uint_as_float((kb & 0x80000000u) ? (kb & 0x7FFFFFFFu) : ~kb);
     a.out_vals[ob + i] = val;
     if (a.out_idx) a.out_idx[ob + i] = idx;
@@ -430,13 +450,13 @@ __global__ __launch_bounds__(kThreads) void row_topk_kernel(TopkArgs a) {
   }
 }
 
-template <int NCH, bool FULL>
+template <int NCH, bool FULL, bool LSM = false>
 void launch_pt(const TopkArgs& a, int pt, hipStream_t stream) {
   const dim3 grid(a.R), block(kThreads);
   switch (pt) {
-    case 1: hipLaunchKernelGGL((row_topk_kernel<NCH, 1, FULL>), grid, block, 0, stream, a); break;
-    case 2: hipLaunchKernelGGL((row_topk_kernel<NCH, 2, FULL>), grid, block, 0, stream, a); break;
-    default: hipLaunchKernelGGL((row_topk_kernel<NCH, 4, FULL>), grid, block, 0, stream, a); break;
+    case 1: hipLaunchKernelGGL((row_topk_kernel<NCH, 1, FULL, LSM>), grid, block, 0, stream, a); break;
+    case 2: hipLaunchKernelGGL((row_topk_kernel<NCH, 2, FULL, LSM>), grid, block, 0, stream, a); break;
+    default: hipLaunchKernelGGL((row_topk_kernel<NCH, 4, FULL, LSM>), grid, block, 0, stream, a); break;
   }
 }
 
@@ -476,4 +496,32 @@ extern "C" int fr_row_topk(const float* x, int64_t ldx, int64_t R, int64_t V, in
   if (chunks <= 4) return launch_nch<4>(a, pt, stream);
   if (chunks <= 8) return launch_nch<8>(a, pt, stream);
   return launch_nch<16>(a, pt, stream);
+}
+
+extern "C" int fr_log_softmax_row_topk(const float* logits, int64_t ldx, int64_t R, int64_t V, int64_t C,
+                                       const int64_t* cand_ids, float* out_vals, int64_t* out_idx,
+                                       int64_t* out_tokens, void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (R < 0 || V <= 0 || C <= 0 || ldx < V) return FR_EINVAL;
+  if (R == 0) return FR_OK;
+  if (!logits || !out_vals) return FR_EINVAL;
+  // the widths fr_log_softmax_f32 runs as one workgroup per row (whose
+  // arithmetic block_row_lse is), whole aligned rows
+  const bool aligned = (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && (ldx & 3) == 0;
+  if (!aligned || (V != 4096 && V != 8192) || C > V || C > kMaxC || R > 0x7FFFFFFF) return FR_EUNSUPPORTED;
+  TopkArgs a{};
+  a.x = logits;
+  a.ldx = ldx;
+  a.cand_ids = cand_ids;
+  a.out_vals = out_vals;
+  a.out_idx = out_idx;
+  a.out_tok = out_tokens;
+  a.R = static_cast<int>(R);
+  a.V = static_cast<int>(V);
+  a.C = static_cast<int>(C);
+  a.vec = 1;
+  const int pt = C <= 256 ? 1 : (C <= 512 ? 2 : 4);
+  if (V == 4096) launch_pt<4, true, true>(a, pt, stream);
+  else launch_pt<8, true, true>(a, pt, stream);
+  return hipGetLastError() == hipSuccess ? FR_OK : FR_ELAUNCH;
 }

@@ -300,6 +300,11 @@ class Qwen3FP8DecodeStep:
 
     def forward(self, x: Optional[torch.Tensor] = None, layers: Optional[int] = None) -> torch.Tensor:
         """Decoder layers, final norm, SID-restricted fp8 lm_head -> logprobs [rows, sid_tokens]."""
+        logprobs, _ = self.lm_head.compute(self._hidden_out(x, layers), self.embed)
+        return logprobs
+
+    def _hidden_out(self, x: Optional[torch.Tensor] = None, layers: Optional[int] = None) -> torch.Tensor:
+        """Decoder layers and the final norm: the lm_head's input."""
         x = self.hidden_in if x is None else x
         residual = None
         # the residual stream is updated in place by the fused add-norms: start
@@ -308,11 +313,9 @@ class Qwen3FP8DecodeStep:
         for L in self.layers[: layers if layers is not None else len(self.layers)]:
             x, residual = self._layer(L, x, residual)
         if x is None:  # folded layers: the stream already holds the last sum
-            y = self.final_norm(residual)
-        else:
-            y, _ = self.final_norm(x, residual)
-        logprobs, _ = self.lm_head.compute(y, self.embed)
-        return logprobs
+            return self.final_norm(residual)
+        y, _ = self.final_norm(x, residual)
+        return y
 
     # ---------------------------------------------------------- graph
     # ---------------------------------------------------------- beam tail
@@ -365,17 +368,20 @@ class Qwen3FP8DecodeStep:
         self._topk_vals = torch.empty(n, bw, self.beam_cand, dtype=torch.float32, device=dev)
         self._topk_tok = torch.empty(n, bw, self.beam_cand, dtype=torch.int64, device=dev)
 
-    def beam_step(self, logprobs: torch.Tensor):
+    def beam_step(self, logprobs: torch.Tensor, from_logits: bool = False):
         """The step's tail (scheduler.py:1469-1561): per-row top-C of the SID
         log-probs with the candidate-id gather, then the fused trie mask +
-        top-K + token-row expand + node advance for every request."""
+        top-K + token-row expand + node advance for every request.  With
+        ``from_logits`` the input is the head's logits and the log-softmax is
+        folded into the top-C (the same log-probs, never written out)."""
         from flashrec_amd.kernel.beam_trie import genrec_mask_topk_expand, row_topk
 
         if self.trie is None:
             raise RuntimeError("built without a trie (trie_items=0)")
         n, bw, c = self.beam_n, self.beam_bw, self.beam_cand
         vals, _, toks = row_topk(logprobs.view(n, bw, -1), c, self.cand_ids,
-                                 out=(self._topk_vals, None), out_tokens=self._topk_tok, need_idx=False)
+                                 out=(self._topk_vals, None), out_tokens=self._topk_tok, need_idx=False,
+                                 log_softmax=from_logits)
         tr = self.trie
         return genrec_mask_topk_expand(
             self.beam_cum, vals, toks, select_k=bw, node_ids=self.beam_nodes, allow_table=tr["allow"],
@@ -383,8 +389,10 @@ class Qwen3FP8DecodeStep:
             invalid_node=tr["invalid"], workspace=self.beam_ws)
 
     def forward_beam(self):
-        """forward() then beam_step(): one whole decode step of beam search."""
-        return self.beam_step(self.forward())
+        """forward() then beam_step(): one whole decode step of beam search,
+        with the head's log-softmax folded into the beam tail's top-C."""
+        logits, _ = self.lm_head.compute_logits(self._hidden_out(), self.embed)
+        return self.beam_step(logits, from_logits=True)
 
     @classmethod
     def from_pretrained(cls, model_path: str, requests: int, beams: int, prefix: int, step: int = 1,

@@ -16,7 +16,7 @@ from typing import Dict, NamedTuple, Optional, Tuple, Union
 
 import torch
 
-from flashrec_amd._lib import call, load, require_device, stream_of
+from flashrec_amd._lib import Unsupported, call, load, require_device, stream_of
 
 
 class GenrecFusedResult(NamedTuple):
@@ -191,6 +191,7 @@ def row_topk(
     out: Optional[Tuple[torch.Tensor, Optional[torch.Tensor]]] = None,
     out_tokens: Optional[torch.Tensor] = None,
     need_idx: bool = True,
+    log_softmax: bool = False,
 ) -> Tuple[torch.Tensor, Optional[torch.Tensor], torch.Tensor]:
     """Sorted top-``k`` over the last dim of fp32 ``scores`` [..., V] and the
     candidate-id gather: (vals, idx, tokens) with tokens = cand_ids[idx] (idx
@@ -200,6 +201,11 @@ def row_topk(
     are caller-owned buffers (graph-capture safe), as in graph.py:186-193.
     With ``need_idx=False`` the column indices are not written and idx is
     None (the beam step consumes only scores and tokens).
+    With ``log_softmax=True`` ``scores`` are logits and the top-``k`` is taken
+    over ``log_softmax(scores, -1)`` (logits.py:118-120 then the top-k),
+    bit-identical to ``log_softmax_f32`` then ``row_topk``; for V = 4096 and
+    8192 the log-probs are formed in registers and never written
+    (``fr_log_softmax_row_topk``), other widths run the two calls.
     k <= min(V, 1024), V <= 16384."""
     require_device(scores)
     if scores.dtype != torch.float32:
@@ -227,10 +233,19 @@ def row_topk(
         cid = _i64(cand_ids.reshape(-1))
         if int(cid.numel()) < v:
             raise ValueError(f"cand_ids has {cid.numel()} entries for {v} columns")
-    call("fr_row_topk", x.data_ptr(), x.stride(0) if r > 1 else v, r, v, int(k),
-         0 if cid is None else cid.data_ptr(), vals.data_ptr(), 0 if idx is None else idx.data_ptr(),
-         tokens.data_ptr(),
-         stream_of(scores))
+    ldx = x.stride(0) if r > 1 else v
+    outs = (0 if cid is None else cid.data_ptr(), vals.data_ptr(), 0 if idx is None else idx.data_ptr(),
+            tokens.data_ptr(), stream_of(scores))
+    if log_softmax:
+        try:
+            call("fr_log_softmax_row_topk", x.data_ptr(), ldx, r, v, int(k), *outs)
+            return vals, idx, tokens
+        except Unsupported:
+            from flashrec_amd.kernel.sglops import log_softmax_f32
+
+            x = log_softmax_f32(x)
+            ldx = x.stride(0) if r > 1 else v
+    call("fr_row_topk", x.data_ptr(), ldx, r, v, int(k), *outs)
     return vals, idx, tokens
 
 

@@ -56,14 +56,20 @@ class _RowBlock:
 
         return _RowBlock(cut(self.weight), cut(self.ids), cut(self.codes), cut(self.scale))
 
+    def logits(self, hidden: torch.Tensor) -> torch.Tensor:
+        """fp32 logits [T, n] of these rows (before the log-softmax)."""
+        if self.codes is None:
+            return F.linear(hidden.to(dtype=self.weight.dtype), self.weight).float()
+        rows = hidden.reshape(-1, hidden.shape[-1])
+        a_codes, a_scale = per_token_quant_fp8(rows)
+        return fp8_scaled_mm(a_codes, self.codes.t(), a_scale, self.scale, torch.float32)
+
     def logprobs(self, hidden: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         if self.codes is None:
             logits = F.linear(hidden.to(dtype=self.weight.dtype), self.weight)
             lp = F.log_softmax(logits.float(), dim=-1)
             return lp if out is None else out.copy_(lp)
-        rows = hidden.reshape(-1, hidden.shape[-1])
-        a_codes, a_scale = per_token_quant_fp8(rows)
-        logits = fp8_scaled_mm(a_codes, self.codes.t(), a_scale, self.scale, torch.float32)
+        logits = self.logits(hidden)
         direct = (out is not None and out.dtype == torch.float32 and out.shape == logits.shape
                   and out.stride(1) == 1 and out.device == logits.device)
         if out is None or direct:
@@ -154,6 +160,16 @@ class RestrictedLMHead:
             return self._head.logprobs(hidden), self._head.ids
         logits = F.linear(hidden.to(dtype=lm_weight.dtype), lm_weight)
         return F.log_softmax(logits.float(), dim=-1), None
+
+    def compute_logits(self, hidden: torch.Tensor, lm_weight: torch.Tensor
+                       ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+        """``compute`` without the log-softmax: (fp32 logits, their ids), for a
+        caller that folds the log-softmax into its top-k
+        (``row_topk(..., log_softmax=True)``)."""
+        self.bind(lm_weight)
+        if self.ready:
+            return self._head.logits(hidden), self._head.ids
+        return F.linear(hidden.to(dtype=lm_weight.dtype), lm_weight).float(), None
 
     def compute_level(self, hidden: torch.Tensor, level: int) -> Tuple[torch.Tensor, torch.Tensor]:
         """Logprobs against one codebook level's rows only."""

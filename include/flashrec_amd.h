@@ -335,6 +335,16 @@ int fr_row_topk(const float* x, int64_t ldx, int64_t R, int64_t V, int64_t C,
 int fr_log_softmax_f32(const float* x, int64_t ldx, float* out, int64_t ldo, int64_t M,
                        int64_t N, void* stream);
 
+/* fr_row_topk over log_softmax(logits) without writing the log-probs: the
+ * decode step's "log_softmax of the SID head (python/flashrec/logits.py:118-120),
+ * then torch.topk + the candidate gather (scheduler.py:1476-1481)".  Outputs
+ * are bit-identical to fr_log_softmax_f32 followed by fr_row_topk.  Takes
+ * V = 4096 or 8192 with 16-byte aligned rows (ldx % 4 == 0), else
+ * FR_EUNSUPPORTED (run the two calls). */
+int fr_log_softmax_row_topk(const float* logits, int64_t ldx, int64_t R, int64_t V, int64_t C,
+                            const int64_t* cand_ids, float* out_vals, int64_t* out_idx,
+                            int64_t* out_tokens, void* stream);
+
 /* Measurement only, no counterpart in the reference: `blocks` workgroups of
  * four waves each run `iters` rounds of four v_mfma_scale_f32_32x32x64_f8f6f4
  * (2 * 32 * 32 * 64 flops each) on register operands, random e4m3 bytes when

@@ -161,3 +161,37 @@ def test_without_indices(dev):
     v1, i1, t1 = row_topk(x, 200, torch.arange(3000, device=dev) * 3, need_idx=False)
     assert i1 is None
     assert torch.equal(v0, v1) and torch.equal(t0, t1) and torch.equal(t0, i0 * 3)
+
+
+@pytest.mark.parametrize("v", [4096, 8192, 2000])
+def test_log_softmax_folded(dev, v):
+    """row_topk(logits, log_softmax=True) (fr_log_softmax_row_topk for V = 4096
+    and 8192; the two calls otherwise) is bit-identical to log_softmax_f32
+    then row_topk, which is held to the oracle here as well; rows with heavy
+    ties, -inf entries, a -inf row and a NaN included."""
+    from flashrec_amd.kernel.beam_trie import row_topk
+    from flashrec_amd.kernel.sglops import log_softmax_f32
+
+    g = torch.Generator().manual_seed(v)
+    x = torch.randn(40, v, generator=g) * 3
+    x[0] = torch.round(x[0])  # heavy ties
+    x[1, ::3] = float("-inf")
+    x[2] = float("-inf")
+    x[3, 17] = float("nan")
+    x[4, :] = 0.0
+    cand = torch.randint(0, 10 ** 6, (v,), generator=g)
+    xd, cd = x.to(dev), cand.to(dev)
+    lp = log_softmax_f32(xd)
+    for k in (1, 200, 512, 1024):
+        print(f"log_softmax folded top-k V={v} k={k}", flush=True)
+        rv, ri, rt = row_topk(lp, k, cd)
+        fv, fi, ft = row_topk(xd, k, cd, log_softmax=True)
+        assert torch.equal(fv.cpu().view(torch.int32), rv.cpu().view(torch.int32))
+        assert torch.equal(fi.cpu(), ri.cpu()) and torch.equal(ft.cpu(), rt.cpu())
+        ov, oi, ot = beam.row_topk(lp.cpu(), k, cand)
+        assert torch.equal(rv.cpu().view(torch.int32), ov.view(torch.int32)) and torch.equal(ri.cpu(), oi)
+    # a strided view (rows not 16-byte aligned) takes the two calls
+    wide = torch.randn(8, v + 1, generator=g).to(dev)[:, 1:]
+    fv, fi, _ = row_topk(wide, 64, log_softmax=True)
+    rv, ri, _ = row_topk(log_softmax_f32(wide.contiguous()), 64)
+    assert torch.equal(fv.cpu().view(torch.int32), rv.cpu().view(torch.int32)) and torch.equal(fi.cpu(), ri.cpu())

@@ -110,6 +110,23 @@ def test_silu_gemm_abi_rejects_bad_shapes():
         _lib.FR_EUNSUPPORTED
 
 
+def test_log_softmax_topk_abi_checks():
+    """fr_log_softmax_row_topk: bad sizes are FR_EINVAL, widths other than
+    4096 / 8192 and unaligned rows FR_EUNSUPPORTED (the caller runs the two
+    calls), all before any launch."""
+    from flashrec_amd import _lib
+
+    lib = _lib.load()
+    p = 4096
+    assert lib.fr_log_softmax_row_topk(p, 8192, 4, 0, 8, p, p, p, p, None) == _lib.FR_EINVAL
+    assert lib.fr_log_softmax_row_topk(p, 100, 4, 8192, 8, p, p, p, p, None) == _lib.FR_EINVAL
+    assert lib.fr_log_softmax_row_topk(p, 2000, 4, 2000, 8, p, p, p, p, None) == _lib.FR_EUNSUPPORTED
+    assert lib.fr_log_softmax_row_topk(p + 4, 8192, 4, 8192, 8, p, p, p, p, None) == _lib.FR_EUNSUPPORTED
+    assert lib.fr_log_softmax_row_topk(p, 8193, 4, 8192, 8, p, p, p, p, None) == _lib.FR_EUNSUPPORTED
+    assert lib.fr_log_softmax_row_topk(p, 8192, 4, 8192, 2048, p, p, p, p, None) == _lib.FR_EUNSUPPORTED
+    assert lib.fr_log_softmax_row_topk(p, 8192, 0, 8192, 8, p, p, p, p, None) == _lib.FR_OK
+
+
 def test_silu_gemm_wrapper_checks_before_the_device():
     """fp8_scaled_mm_silu refuses wrong dtypes, mismatched K and N not a multiple of 16 before any launch."""
     from flashrec_amd.kernel.sglops import fp8_scaled_mm_silu
