@@ -303,8 +303,11 @@ class Qwen3FP8DecodeStep:
         logprobs, _ = self.lm_head.compute(self._hidden_out(x, layers), self.embed)
         return logprobs
 
-    def _hidden_out(self, x: Optional[torch.Tensor] = None, layers: Optional[int] = None) -> torch.Tensor:
-        """Decoder layers and the final norm: the lm_head's input."""
+    def _hidden_out(self, x: Optional[torch.Tensor] = None, layers: Optional[int] = None,
+                    quant: bool = False):
+        """Decoder layers and the final norm: the lm_head's input (with
+        ``quant``, as per-token e4m3 codes and scales from the fused
+        RMSNorm -> e4m3, the rows the fp8 head would quantise)."""
         x = self.hidden_in if x is None else x
         residual = None
         # the residual stream is updated in place by the fused add-norms: start
@@ -313,7 +316,10 @@ class Qwen3FP8DecodeStep:
         for L in self.layers[: layers if layers is not None else len(self.layers)]:
             x, residual = self._layer(L, x, residual)
         if x is None:  # folded layers: the stream already holds the last sum
-            return self.final_norm(residual)
+            return self.final_norm.quant_fp8(residual) if quant else self.final_norm(residual)
+        if quant:
+            q, s, _ = self.final_norm.quant_fp8(x, residual)
+            return q, s
         y, _ = self.final_norm(x, residual)
         return y
 
@@ -390,8 +396,10 @@ class Qwen3FP8DecodeStep:
 
     def forward_beam(self):
         """forward() then beam_step(): one whole decode step of beam search,
-        with the head's log-softmax folded into the beam tail's top-C."""
-        logits, _ = self.lm_head.compute_logits(self._hidden_out(), self.embed)
+        with the final norm writing the fp8 head's e4m3 input directly and the
+        head's log-softmax folded into the beam tail's top-C."""
+        q, s = self._hidden_out(quant=True)
+        logits, _ = self.lm_head.compute_logits_fp8(q, s, self.embed)
         return self.beam_step(logits, from_logits=True)
 
     @classmethod

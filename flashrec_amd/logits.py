@@ -61,7 +61,10 @@ class _RowBlock:
         if self.codes is None:
             return F.linear(hidden.to(dtype=self.weight.dtype), self.weight).float()
         rows = hidden.reshape(-1, hidden.shape[-1])
-        a_codes, a_scale = per_token_quant_fp8(rows)
+        return self.logits_fp8(*per_token_quant_fp8(rows))
+
+    def logits_fp8(self, a_codes: torch.Tensor, a_scale: torch.Tensor) -> torch.Tensor:
+        """fp32 logits from hidden rows already quantised per token (fp8 heads)."""
         return fp8_scaled_mm(a_codes, self.codes.t(), a_scale, self.scale, torch.float32)
 
     def logprobs(self, hidden: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -170,6 +173,17 @@ class RestrictedLMHead:
         if self.ready:
             return self._head.logits(hidden), self._head.ids
         return F.linear(hidden.to(dtype=lm_weight.dtype), lm_weight).float(), None
+
+    def compute_logits_fp8(self, a_codes: torch.Tensor, a_scale: torch.Tensor, lm_weight: torch.Tensor
+                           ) -> Tuple[torch.Tensor, torch.Tensor]:
+        """``compute_logits`` for hidden rows already quantised per token (e4m3
+        codes [T, hidden], fp32 scales [T, 1]), e.g. by ``RMSNorm.quant_fp8``:
+        the same logits as ``compute_logits`` on the bf16 rows they came from.
+        fp8 heads only."""
+        self.bind(lm_weight)
+        if not self.ready or self._head.codes is None:
+            raise RuntimeError("compute_logits_fp8 needs a bound fp8 head (RestrictedLMHead(..., fp8=True))")
+        return self._head.logits_fp8(a_codes, a_scale), self._head.ids
 
     def compute_level(self, hidden: torch.Tensor, level: int) -> Tuple[torch.Tensor, torch.Tensor]:
         """Logprobs against one codebook level's rows only."""

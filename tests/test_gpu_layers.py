@@ -118,6 +118,21 @@ def test_restricted_lm_head_fp8(dev):
     ref1 = ops.restricted_logprobs_fp8(h, w[lo + 4096:lo + 6144])
     assert ids1.cpu().tolist() == list(range(lo + 4096, lo + 6144))
     assert (lp1.cpu() - ref1).abs().max().item() < 2e-3
+    # logits without the log-softmax, from bf16 rows or from rows quantised
+    # by the fused RMSNorm -> e4m3: the same bits as the norm then the head
+    from flashrec_amd.kernel.sglops import log_softmax_f32, rmsnorm
+    from flashrec_amd.layers.norm import RMSNorm
+
+    lg, ids2 = head.compute_logits(h.to(dev), w.to(dev))
+    assert torch.equal(ids2.cpu(), ids.cpu())
+    assert torch.equal(log_softmax_f32(lg).cpu(), lp.cpu())
+    norm = RMSNorm(hidden)
+    norm.weight = torch.nn.Parameter((1 + 0.1 * torch.randn(hidden, generator=g)).to(torch.bfloat16).to(dev),
+                                     requires_grad=False)
+    x = (3 * torch.randn(64, hidden, generator=g)).to(torch.bfloat16).to(dev)
+    want, _ = head.compute_logits(rmsnorm(x, norm.weight, norm.eps), w.to(dev))
+    got, _ = head.compute_logits_fp8(*norm.quant_fp8(x), w.to(dev))
+    assert torch.equal(got.cpu().view(torch.int32), want.cpu().view(torch.int32))
 
 
 def test_graph_capture_replays(dev):
