@@ -200,6 +200,19 @@ def attention_plan(kv_indices: torch.Tensor, kv_start: torch.Tensor, kv_len: tor
     return out
 
 
+def _check_plan(group_prefix: Optional[torch.Tensor], T: int, hq: int, hk: int) -> int:
+    """The plan's device pointer (0 for none) after checking it holds the
+    entries the kernels read for T tokens."""
+    if group_prefix is None:
+        return 0
+    n = plan_size(T, hq, hk)
+    if group_prefix.dtype != torch.int32 or not group_prefix.is_contiguous() or group_prefix.numel() < n:
+        raise ValueError(f"group_prefix must be a contiguous int32 plan of at least {n} entries "
+                         "(attention_plan over the same slot lists)")
+    require_device(group_prefix)
+    return group_prefix.data_ptr()
+
+
 def _check_attention_inputs(q, k_cache, v_cache, kv_indices, kv_start, kv_len):
     require_device(q, k_cache, v_cache, kv_indices, kv_start, kv_len)
     if q.dtype != torch.bfloat16:
@@ -248,7 +261,7 @@ def paged_attention_quant_fp8(q: torch.Tensor, k_cache: torch.Tensor, v_cache: t
              v_cache.data_ptr(), v_cache.stride(0), v_cache.stride(1),
              slots, kv_indices.data_ptr(), kv_start.data_ptr(), kv_len.data_ptr(),
              out.data_ptr(), out.stride(0), out_scale.data_ptr(),
-             T, Hq, Hk, D, float(scale), 0 if group_prefix is None else group_prefix.data_ptr(), stream_of(q))
+             T, Hq, Hk, D, float(scale), _check_plan(group_prefix, T, Hq, Hk), stream_of(q))
     except Unsupported:
         from flashrec_amd.kernel.sglops import per_token_quant_fp8
 
@@ -279,5 +292,5 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
          v_cache.data_ptr(), v_cache.stride(0), v_cache.stride(1),
          slots, kv_indices.data_ptr(), kv_start.data_ptr(), kv_len.data_ptr(),
          out.data_ptr(), out.stride(0), out.stride(1),
-         T, Hq, Hk, D, float(scale), 0 if group_prefix is None else group_prefix.data_ptr(), stream_of(q))
+         T, Hq, Hk, D, float(scale), _check_plan(group_prefix, T, Hq, Hk), stream_of(q))
     return out

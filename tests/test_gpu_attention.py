@@ -244,6 +244,8 @@ def test_grouped_prefixes_with_ragged_suffixes(dev, hq, hk):
     d = [t.to(dev) for t in (q, k, v, idx, start, ln)]
     gp = attention_plan(d[3], d[4], d[5], hq, hk)
     assert torch.equal(paged_attention(*d, SCALE, group_prefix=gp).cpu(), got.cpu())
+    with pytest.raises(ValueError, match="plan"):  # a plan shorter than the groups is refused
+        paged_attention(*d, SCALE, group_prefix=gp[:-1])
     expect = []
     for g0 in range(0, len(rows), tok):
         grp_rows = rows[g0: g0 + tok]
