@@ -147,12 +147,16 @@ def genrec_mask_topk_expand(
     if expand_i:
         tok_in, tok_out = _pingpong(ws, "tok", _i64(token_ids), torch.int64)
         width = int(tok_in.shape[-1])
-    col_t = ws.get("col", (n,), torch.int32, dev)
-    if isinstance(col, torch.Tensor):
-        src = col.to(device=dev, dtype=torch.int32).reshape(-1)
-        col_t.copy_(src.expand(n) if src.numel() == 1 else src[:n])
+    if (isinstance(col, torch.Tensor) and col.device == dev and col.dtype == torch.int32
+            and col.is_contiguous() and col.numel() == n):
+        col_t = col  # read only (const int32_t* col): no staging copy
     else:
-        col_t.fill_(int(col))
+        col_t = ws.get("col", (n,), torch.int32, dev)
+        if isinstance(col, torch.Tensor):
+            src = col.to(device=dev, dtype=torch.int32).reshape(-1)
+            col_t.copy_(src.expand(n) if src.numel() == 1 else src[:n])
+        else:
+            col_t.fill_(int(col))
     do_exp = None
     if do_expand is not None:
         do_exp = do_expand.to(device=dev, dtype=torch.uint8).reshape(-1).contiguous()
