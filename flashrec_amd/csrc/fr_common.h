@@ -47,7 +47,7 @@ __device__ __forceinline__ void stnt(T* p, T v) {
 // Plain load for input that a later kernel of the decode step reads again
 // (the residual stream, the queries rotated in place, the head's logits):
 // a nontemporal load leaves the lines out of the caches, so the next reader
-// goes to HBM; a plain one keeps them (config-4 step 8.46 -> 8.37 ms).
+// goes to HBM; a plain one keeps them (the config-4 decode step: 1.3 % faster).
 template <typename T>
 __device__ __forceinline__ T ldkeep(const T* p) {
   return *p;
