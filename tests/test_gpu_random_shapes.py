@@ -120,3 +120,34 @@ def test_random_row_quantizers(dev, seed):
         q, s = silu_and_mul_per_token_quant_fp8(xs.to(dev))
         q_ref, s_ref = ops.silu_and_mul_per_token_quant_fp8(xs)
     assert_fp8_parity(q, s, q_ref, s_ref, label=f"{kind} {m}x{k} {dt} x{sc}")
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_log_softmax_topk(dev, seed):
+    """row_topk with the log-softmax folded in, bit-identical to log_softmax_f32
+    then row_topk, which is held to the oracle's top-k: random row counts,
+    widths 4096 / 8192 (the folded kernel) and others (the two calls), k up
+    to 1024, logit scales that make ties and underflowing exp."""
+    from oracle import beam
+
+    from flashrec_amd.kernel.beam_trie import row_topk
+    from flashrec_amd.kernel.sglops import log_softmax_f32
+
+    rnd = random.Random(seed)
+    r = rnd.choice([1, 3, 64, 257, 1024])
+    v = rnd.choice([4096, 8192, 8192, 1000])
+    k = rnd.choice([1, 7, 256, 300, 512, 1000])
+    sc = rnd.choice([0.5, 4.0, 60.0])
+    g = torch.Generator().manual_seed(4000 + seed)
+    x = torch.randn(r, v, generator=g) * sc
+    if seed % 2:
+        x = torch.round(x)  # ties
+    cand = torch.randint(0, 10 ** 6, (v,), generator=g)
+    xd, cd = x.to(dev), cand.to(dev)
+    lp = log_softmax_f32(xd)
+    fv, fi, ft = row_topk(xd, k, cd, log_softmax=True)
+    rv, ri, rt = row_topk(lp, k, cd)
+    assert torch.equal(fv.cpu().view(torch.int32), rv.cpu().view(torch.int32))
+    assert torch.equal(fi.cpu(), ri.cpu()) and torch.equal(ft.cpu(), rt.cpu())
+    ov, oi, _ = beam.row_topk(lp.cpu(), k, cand)
+    assert torch.equal(rv.cpu().view(torch.int32), ov.view(torch.int32)) and torch.equal(ri.cpu(), oi)
