@@ -56,6 +56,8 @@ SIGNATURES = {
         _I64, _I64, _I64, _I64, _P,  # T, Hq, Hk, D, stream
     ],
     "fr_rope_inplace": [_P, _I64, _I64, _P, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _P],
+    "fr_rope_inplace_any": [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I32, _P, _P, _I64, _I64, _I64, _I64, _I64,
+                            _P],
     "fr_store_kv_fp8": [_P, _I64, _P, _I64, _I32, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _P],
     "fr_store_kv_bf16": [_P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _P],
     "fr_rope_store_kv_bf16": [

@@ -144,6 +144,10 @@ template <>
 struct Elem<FR_DTYPE_FP32> {
   using T = float;
   static __device__ __forceinline__ float load(const T* p) { return *p; }
+  // fp32 activations keep their intermediates in fp32 (torch's `.to(x.dtype)`
+  // is then the identity)
+  static __device__ __forceinline__ float round(float x) { return x; }
+  static __device__ __forceinline__ float bits(float x) { return x; }
 };
 
 // ---------------------------------------------------------------- e4m3

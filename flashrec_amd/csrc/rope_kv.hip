@@ -82,8 +82,12 @@ __global__ __launch_bounds__(256) void qk_rope_kv_d128(RopeArgs a) {
   const int j = lane & 15;   // 8-element chunk inside the head
   const int e0 = j * 8;
 
+  // a token whose position has no cos/sin row writes neither its K nor its
+  // V row (the slot keeps its old contents rather than a new V beside an
+  // old K)
   const int64_t slot = STORE ? a.loc[t] : 0;
-  const bool slot_ok = slot >= 0 && slot < a.num_slots;
+  const int64_t tpos = a.pos[t];
+  const bool slot_ok = slot >= 0 && slot < a.num_slots && tpos >= 0 && tpos < a.cs_rows;
 
   if (STORE && g >= qg + kg) {  // V: e4m3 conversion or bf16 copy into the slot
     if (!slot_ok) return;
@@ -204,7 +208,8 @@ __global__ __launch_bounds__(256) void qk_rope_kv_generic(RopeArgs a) {
   const int half = a.D >> 1;
   const bool active = lane < half;
   const int64_t slot = STORE ? a.loc[t] : 0;
-  const bool slot_ok = slot >= 0 && slot < a.num_slots;
+  const int64_t tpos = a.pos[t];
+  const bool slot_ok = slot >= 0 && slot < a.num_slots && tpos >= 0 && tpos < a.cs_rows;
   if (STORE && hh >= a.Hq + a.Hk) {
     const int h = hh - a.Hq - a.Hk;
     if (!slot_ok || !active) return;
@@ -256,6 +261,52 @@ __global__ __launch_bounds__(256) void qk_rope_kv_generic(RopeArgs a) {
     uint8_t* dst = a.kc + slot * a.sckp + h * a.sckh;
     dst[lane] = static_cast<uint8_t>(e4m3_torch_byte(y1));
     dst[lane + half] = static_cast<uint8_t>(e4m3_torch_byte(y2));
+  }
+}
+
+// NeoX rotate-half RoPE in place for layouts the kernels above do not take:
+// bf16, fp16 or fp32 heads, any even D, any element strides.  One wave per
+// (token, head), lane i walking the rotate-half pairs (i, i + D/2) with a
+// stride of 64.  The arithmetic is torch's for a head of that dtype times
+// the fp32 cos/sin rows: y1 = x1*c - x2*s, y2 = x2*c + x1*s in fp32, then one
+// rounding to the head's dtype (none for fp32).
+struct RopeAnyArgs {
+  void* q;
+  int64_t sqt, sqh, sqd;
+  void* k;
+  int64_t skt, skh, skd;
+  const int64_t* pos;
+  const float* cs;
+  int64_t cs_rows;
+  int64_t T;
+  int Hq, Hk, D;
+};
+
+template <int DT>
+__global__ __launch_bounds__(256) void rope_inplace_any(RopeAnyArgs a) {
+  using E = Elem<DT>;
+  using T = typename E::T;
+  const int lane = threadIdx.x & 63;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int per_tok = a.Hq + a.Hk;
+  const int64_t t = item / per_tok;
+  if (t >= a.T) return;
+  const int hh = static_cast<int>(item - t * per_tok);
+  const int64_t pos = a.pos[t];
+  if (pos < 0 || pos >= a.cs_rows) return;
+  const bool is_q = hh < a.Hq;
+  const int h = is_q ? hh : hh - a.Hq;
+  T* x = is_q ? static_cast<T*>(a.q) + t * a.sqt + h * a.sqh : static_cast<T*>(a.k) + t * a.skt + h * a.skh;
+  const int64_t sd = is_q ? a.sqd : a.skd;
+  const int half = a.D >> 1;
+  const float* csr = a.cs + pos * a.D;
+  for (int i = lane; i < half; i += 64) {
+    const float x1 = E::load(x + i * sd), x2 = E::load(x + (i + half) * sd);
+    const float c = csr[i], s = csr[half + i];
+    const float y1 = x1 * c - x2 * s;
+    const float y2 = x2 * c + x1 * s;
+    x[i * sd] = E::bits(y1);
+    x[(i + half) * sd] = E::bits(y2);
   }
 }
 
@@ -423,6 +474,38 @@ int fr_rope_inplace(void* q, int64_t sqt, int64_t sqh, void* k, int64_t skt, int
     const int64_t items = T * (Hq + Hk);
     hipLaunchKernelGGL(qk_rope_kv_generic<kRope>, dim3(static_cast<unsigned>((items + 3) / 4)),
                        dim3(256), 0, st, a);
+  }
+  return hipGetLastError() == hipSuccess ? FR_OK : FR_ELAUNCH;
+}
+
+int fr_rope_inplace_any(void* q, int64_t sqt, int64_t sqh, int64_t sqd, void* k, int64_t skt, int64_t skh,
+                        int64_t skd, int dtype, const int64_t* positions, const float* cos_sin_cache,
+                        int64_t cache_rows, int64_t T, int64_t Hq, int64_t Hk, int64_t D, void* stream) {
+  if (T < 0 || Hq < 0 || Hk < 0 || D <= 0 || (D & 1)) return FR_EINVAL;
+  if (dtype != FR_DTYPE_BF16 && dtype != FR_DTYPE_FP16 && dtype != FR_DTYPE_FP32) return FR_EUNSUPPORTED;
+  if (T == 0 || Hq + Hk == 0) return FR_OK;
+  if (!q || !k || !positions || !cos_sin_cache) return FR_EINVAL;
+  // grid of items / 4 workgroups (< 2^31)
+  if (Hq + Hk > 0x7FFFFFFF || T > (int64_t(1) << 33) / (Hq + Hk)) return FR_EUNSUPPORTED;
+  RopeAnyArgs a{};
+  a.q = q;
+  a.sqt = sqt; a.sqh = sqh; a.sqd = sqd;
+  a.k = k;
+  a.skt = skt; a.skh = skh; a.skd = skd;
+  a.pos = positions;
+  a.cs = cos_sin_cache;
+  a.cs_rows = cache_rows;
+  a.T = T;
+  a.Hq = static_cast<int>(Hq);
+  a.Hk = static_cast<int>(Hk);
+  a.D = static_cast<int>(D);
+  const int64_t items = T * (Hq + Hk);
+  const dim3 grid(static_cast<unsigned>((items + 3) / 4));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case FR_DTYPE_BF16: hipLaunchKernelGGL(rope_inplace_any<FR_DTYPE_BF16>, grid, dim3(256), 0, st, a); break;
+    case FR_DTYPE_FP16: hipLaunchKernelGGL(rope_inplace_any<FR_DTYPE_FP16>, grid, dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL(rope_inplace_any<FR_DTYPE_FP32>, grid, dim3(256), 0, st, a); break;
   }
   return hipGetLastError() == hipSuccess ? FR_OK : FR_ELAUNCH;
 }

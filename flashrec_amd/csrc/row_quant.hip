@@ -50,11 +50,6 @@ __device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
   }
 }
 
-__device__ __forceinline__ float silu_bf16(float g) {
-  // torch CPU silu: x / (1 + exp(-x)) in fp32, then the bf16 store.
-  return round_bf16(g / (1.0f + expf(-g)));
-}
-
 // Grid-stride over rows, one wave per row at a time, NV vectors of 8
 // elements per lane held in registers as fp32.  FULL: K == NV * 512, no
 // per-vector bounds.  The kernels are VALU-issue bound (a wave64 op takes 4
@@ -67,16 +62,26 @@ __device__ __forceinline__ float silu_bf16(float g) {
 // rare row without paying for it in registers.
 //
 // The RMS and SiLU modes round their intermediates to the activation dtype
-// (bf16 or fp16: torch's CPU ops compute in fp32 and store in that dtype);
-// the residual and the norm weight are in that dtype too.
+// (bf16 or fp16: torch's CPU ops compute in fp32 and store in that dtype;
+// fp32 rows keep them unrounded); the residual, the norm weight and the
+// unquantized output rows are in that dtype too.
+//
+// SiLU: the same arithmetic as the vector kernel and the GEMM's SiLU
+// epilogue (silu_in_range for |g| <= 80, torch's formula beyond), so a row
+// gives the same bits whichever kernel takes it.
+__device__ __forceinline__ float silu_any(float g) {
+  return __builtin_fabsf(g) <= 80.0f ? silu_in_range(g) : g / (1.0f + expf(-g));
+}
+
 template <int MODE, int DT, bool QOUT>
 __device__ __forceinline__ void generic_row(const RowArgs& a, int64_t row, int lane) {
   using E = Elem<DT>;
   using T = typename E::T;
-  using H = Elem<DT == FR_DTYPE_FP32 ? FR_DTYPE_BF16 : DT>;  // 16-bit dtype of the RMS/SiLU modes
+  using H = E;  // dtype of the RMS/SiLU intermediates
   const int64_t K = a.K;
   const T* xr = reinterpret_cast<const T*>(a.x) + row * a.ldx;
-  uint16_t* rr = (MODE == kAddRms) ? a.res + row * a.ldr : nullptr;
+  T* rr = (MODE == kAddRms) ? reinterpret_cast<T*>(a.res) + row * a.ldr : nullptr;
+  const T* wr = reinterpret_cast<const T*>(a.w);
 
   // Pass 1: the pre-normalisation value of each element (and the residual
   // update), plus the sum of squares.
@@ -101,13 +106,13 @@ __device__ __forceinline__ void generic_row(const RowArgs& a, int64_t row, int l
     } else {
       val = E::load(xr + e);
     }
-    if (MODE == kSilu) val = H::round(H::round(val / (1.0f + expf(-val))) * E::load(xr + K + e));
-    if (MODE == kRms || MODE == kAddRms) val = H::round((val * rstd) * H::load(a.w + e));
+    if (MODE == kSilu) val = H::round(H::round(silu_any(val)) * E::load(xr + K + e));
+    if (MODE == kRms || MODE == kAddRms) val = H::round((val * rstd) * H::load(wr + e));
     return val;
   };
 
   if (!QOUT) {
-    uint16_t* orow = reinterpret_cast<uint16_t*>(a.q) + row * a.ldq;
+    T* orow = reinterpret_cast<T*>(a.q) + row * a.ldq;
     for (int64_t e = lane; e < K; e += 64) orow[e] = H::bits(value(e));
     return;
   }
@@ -497,7 +502,6 @@ static int launch_rows(RowArgs a, int dtype, hipStream_t st) {
         hipLaunchKernelGGL((row_kernel_generic<MODE, FR_DTYPE_FP16, QOUT>), grid, dim3(256), 0, st, a);
         break;
       case FR_DTYPE_FP32:
-        if (MODE != kQuant) return FR_EUNSUPPORTED;
         hipLaunchKernelGGL((row_kernel_generic<MODE, FR_DTYPE_FP32, QOUT>), grid, dim3(256), 0, st, a);
         break;
       default:
@@ -535,7 +539,7 @@ int fr_quantize_weight_fp8(const void* w, int w_dtype, int64_t N, int64_t K, int
 
 int fr_rms_quant_fp8(const void* x, int x_dtype, int64_t ldx, void* residual, int64_t ldr,
                      const void* w, int64_t M, int64_t H, float eps, void* q, float* s, void* stream) {
-  if (x_dtype != FR_DTYPE_BF16 && x_dtype != FR_DTYPE_FP16) return FR_EUNSUPPORTED;
+  if (x_dtype != FR_DTYPE_BF16 && x_dtype != FR_DTYPE_FP16 && x_dtype != FR_DTYPE_FP32) return FR_EUNSUPPORTED;
   if ((M > 0 && H > 0) && (!x || !w || !q || !s)) return FR_EINVAL;
   RowArgs a{};
   a.x = static_cast<const uint16_t*>(x);
@@ -555,7 +559,7 @@ int fr_rms_quant_fp8(const void* x, int x_dtype, int64_t ldx, void* residual, in
 
 int fr_rmsnorm(const void* x, int x_dtype, int64_t ldx, void* residual, int64_t ldr, const void* w,
                void* out, int64_t ldo, int64_t M, int64_t H, float eps, void* stream) {
-  if (x_dtype != FR_DTYPE_BF16 && x_dtype != FR_DTYPE_FP16) return FR_EUNSUPPORTED;
+  if (x_dtype != FR_DTYPE_BF16 && x_dtype != FR_DTYPE_FP16 && x_dtype != FR_DTYPE_FP32) return FR_EUNSUPPORTED;
   if ((M > 0 && H > 0) && (!x || !w || !out)) return FR_EINVAL;
   RowArgs a{};
   a.x = static_cast<const uint16_t*>(x);
@@ -574,7 +578,7 @@ int fr_rmsnorm(const void* x, int x_dtype, int64_t ldx, void* residual, int64_t 
 
 int fr_silu_quant_fp8(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t d, void* q, float* s,
                       void* stream) {
-  if (x_dtype != FR_DTYPE_BF16 && x_dtype != FR_DTYPE_FP16) return FR_EUNSUPPORTED;
+  if (x_dtype != FR_DTYPE_BF16 && x_dtype != FR_DTYPE_FP16 && x_dtype != FR_DTYPE_FP32) return FR_EUNSUPPORTED;
   if ((M > 0 && d > 0) && (!x || !q || !s)) return FR_EINVAL;
   RowArgs a{};
   a.x = static_cast<const uint16_t*>(x);
@@ -589,7 +593,7 @@ int fr_silu_quant_fp8(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_
 
 int fr_silu_and_mul(const void* x, int x_dtype, int64_t ldx, void* out, int64_t ldo, int64_t M, int64_t d,
                     void* stream) {
-  if (x_dtype != FR_DTYPE_BF16 && x_dtype != FR_DTYPE_FP16) return FR_EUNSUPPORTED;
+  if (x_dtype != FR_DTYPE_BF16 && x_dtype != FR_DTYPE_FP16 && x_dtype != FR_DTYPE_FP32) return FR_EUNSUPPORTED;
   if ((M > 0 && d > 0) && (!x || !out)) return FR_EINVAL;
   RowArgs a{};
   a.x = static_cast<const uint16_t*>(x);

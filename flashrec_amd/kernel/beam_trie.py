@@ -12,6 +12,7 @@ PyTorch branch).
 
 from __future__ import annotations
 
+import warnings
 from typing import Dict, NamedTuple, Optional, Tuple, Union
 
 import torch
@@ -432,5 +433,16 @@ def call_genrec_cuda(out_vals, out_parents, out_tokens, out_indices, scratch, cu
     if have >= need:
         rc = lib.fr_genrec_mask_topk_expand(*head, scratch.data_ptr(), have, *args)
     else:
+        global _warned_static_scratch
+        if not _warned_static_scratch:
+            # the static array is one per GPU: beam steps running on two
+            # streams at once would overwrite each other's slice lists
+            warnings.warn(f"genrec scratch of {have} bytes is below the {need} needed; using the library's "
+                          "static per-GPU scratch, which concurrent beam steps on one GPU must not share",
+                          RuntimeWarning, stacklevel=2)
+            _warned_static_scratch = True
         rc = lib.fr_genrec_mask_topk_expand_noalloc(*head, *args)
     return rc == 0
+
+
+_warned_static_scratch = False

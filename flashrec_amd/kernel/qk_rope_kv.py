@@ -28,11 +28,13 @@ def fused_qk_norm_rope_store_fp8(
     k_cache: torch.Tensor,
     v_cache: torch.Tensor,
 ) -> bool:
-    """In-place NeoX RoPE on Q; RMSNorm Q/K; scatter unscaled FP8 K/V.
+    """Per-head RMSNorm of q and k, rotate-half RoPE, q written back in
+    place, K and V stored as e4m3 (scale 1) into their slots ``loc``.
 
-    ``q/k/v`` are ``[T, H, D]`` (strided views allowed, unit inner stride).
-    Caches are ``[pages, H_kv, D]`` fp8.  Returns False when the layout is
-    one the fused op does not take (caller falls back), as the reference does.
+    Heads are ``[T, H, D]`` views whose last dimension is contiguous (views
+    into the fused qkv output need no copy); the pools are ``[slots, H_kv, D]``
+    e4m3.  A layout this kernel does not take returns False before any work,
+    so the caller can run the unfused steps, the reference's contract.
     """
     require_device(q, k, v, k_cache, v_cache)
     if q.numel() == 0:

@@ -2,7 +2,8 @@
 
 Reference: python/flashrec/kernel/rms_fp8.py:74-145.  The reference's CUDA
 path is a Triton kernel that quantizes the fp32 normalised value; its CPU
-path rounds the normalised row to the activation dtype (bf16 or fp16) first (``rmsnorm`` then
+path rounds the normalised row to the activation dtype (bf16 or fp16; fp32 rows
+are not rounded) first (``rmsnorm`` then
 ``per_token_quant_fp8``, rms_fp8.py:128-130 / :141-145).  This kernel
 reproduces the latter bit for bit, in one pass over HBM.
 """
@@ -14,6 +15,7 @@ from typing import Optional
 import torch
 
 from flashrec_amd._lib import DTYPE_CODE, call, require_device, stream_of
+from flashrec_amd.kernel.sglops import _ACT
 
 _FP8_MAX = 448.0
 
@@ -24,9 +26,9 @@ def _launch(
     eps: float,
     residual: Optional[torch.Tensor],
 ) -> tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
+    if x.dtype not in _ACT or (residual is not None and residual.dtype != x.dtype):
+        raise TypeError("rms_fp8 takes bf16, fp16 or fp32 activations (and a residual of the same dtype)")
     require_device(x, residual)
-    if x.dtype not in (torch.bfloat16, torch.float16) or (residual is not None and residual.dtype != x.dtype):
-        raise TypeError("rms_fp8 takes bf16 or fp16 activations (and a residual of the same dtype)")
     orig = x.shape
     hidden = int(weight.numel())
     x2 = x.reshape(-1, hidden).contiguous()

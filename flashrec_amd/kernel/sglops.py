@@ -19,6 +19,10 @@ _FP8_MAX = 448.0
 
 
 _HALF = (torch.bfloat16, torch.float16)
+# activation dtypes of the row kernels (rmsnorm, fused_add_rmsnorm,
+# silu_and_mul and their fp8-quantizing forms): intermediates are rounded to
+# the activation dtype, fp32 rows keep them in fp32
+_ACT = (torch.bfloat16, torch.float16, torch.float32)
 
 
 def _vec(weight: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
@@ -38,8 +42,8 @@ def _rows(x: torch.Tensor, width: int) -> torch.Tensor:
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     """``(x * rsqrt(mean(x^2) + eps)) * weight`` per row (sglops.py:33-45)."""
     require_device(x)
-    if x.dtype not in _HALF:
-        raise TypeError(f"rmsnorm takes bf16/fp16 activations, got {x.dtype}")
+    if x.dtype not in _ACT:
+        raise TypeError(f"rmsnorm takes bf16/fp16/fp32 activations, got {x.dtype}")
     orig = x.shape
     hidden = int(weight.numel())
     x2 = _rows(x, hidden)
@@ -56,8 +60,8 @@ def fused_add_rmsnorm(
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """``residual += x`` then RMSNorm(residual). Mutates both (sglops.py:48-61)."""
     require_device(x, residual)
-    if x.dtype not in _HALF or residual.dtype != x.dtype:
-        raise TypeError("fused_add_rmsnorm takes bf16 or fp16 x and a residual of the same dtype")
+    if x.dtype not in _ACT or residual.dtype != x.dtype:
+        raise TypeError("fused_add_rmsnorm takes bf16, fp16 or fp32 x and a residual of the same dtype")
     hidden = int(weight.numel())
     x2 = x.reshape(-1, hidden).contiguous()
     r2 = residual.reshape(-1, hidden).contiguous()
@@ -97,6 +101,38 @@ def apply_rope_inplace(
          k3.stride(0), k3.stride(1), pos.data_ptr(), cs.data_ptr(), cs.shape[0], t,
          q3.shape[1], k3.shape[1], d, stream_of(query))
     return True
+
+
+def _heads(x: torch.Tensor, t: int, d: int) -> torch.Tensor:
+    """[T, H*D] or [T, H, D] -> a [T, H, D] view (any strides)."""
+    return x.unflatten(-1, (-1, d)) if x.dim() == 2 else x.reshape(t, -1, d)
+
+
+@torch.compiler.disable
+def rope_inplace_any(
+    positions: torch.Tensor,
+    query: torch.Tensor,
+    key: torch.Tensor,
+    head_size: int,
+    cos_sin_cache: torch.Tensor,
+) -> None:
+    """NeoX RoPE in place for the layouts ``apply_rope_inplace`` declines
+    (fp16 / fp32 heads, D > 128, strided head elements): the torch branch of
+    ``RotaryEmbedding.forward`` (python/flashrec/layers/rotary.py:55-71),
+    fp32 products and sums rounded once to the head's dtype."""
+    require_device(query, key)
+    d = int(head_size)
+    if d <= 0 or d % 2 or int(cos_sin_cache.shape[-1]) != d:
+        raise ValueError(f"RoPE needs an even head size matching the cos/sin cache, got {d}")
+    if query.dtype not in _ACT or key.dtype != query.dtype:
+        raise TypeError(f"RoPE takes bf16, fp16 or fp32 heads of one dtype, got {query.dtype} / {key.dtype}")
+    t = int(positions.numel())
+    q3, k3 = _heads(query, t, d), _heads(key, t, d)
+    pos = positions.reshape(-1).to(dtype=torch.int64).contiguous()
+    cs = cos_sin_cache.to(device=query.device, dtype=torch.float32).contiguous()
+    call("fr_rope_inplace_any", q3.data_ptr(), q3.stride(0), q3.stride(1), q3.stride(2), k3.data_ptr(),
+         k3.stride(0), k3.stride(1), k3.stride(2), DTYPE_CODE[query.dtype], pos.data_ptr(), cs.data_ptr(),
+         cs.shape[0], t, q3.shape[1], k3.shape[1], d, stream_of(query))
 
 
 @torch.compiler.disable
@@ -289,8 +325,8 @@ def fp8_scaled_mm_silu(
 def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
     """SwiGLU: ``silu(x[..., :d]) * x[..., d:]`` with ``d = last_dim // 2`` (sglops.py:143-151)."""
     require_device(x)
-    if x.dtype not in _HALF:
-        raise TypeError(f"silu_and_mul takes bf16/fp16, got {x.dtype}")
+    if x.dtype not in _ACT:
+        raise TypeError(f"silu_and_mul takes bf16/fp16/fp32, got {x.dtype}")
     last = int(x.shape[-1])
     if last % 2:
         raise ValueError("silu_and_mul needs an even last dimension")
@@ -424,6 +460,7 @@ __all__ = [
     "rmsnorm",
     "fused_add_rmsnorm",
     "apply_rope_inplace",
+    "rope_inplace_any",
     "per_token_quant_fp8",
     "fp8_scaled_mm",
     "fp8_scaled_mm_silu",

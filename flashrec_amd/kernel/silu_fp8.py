@@ -11,6 +11,7 @@ from __future__ import annotations
 import torch
 
 from flashrec_amd._lib import DTYPE_CODE, call, require_device, stream_of
+from flashrec_amd.kernel.sglops import _ACT
 
 _FP8_MAX = 448.0
 
@@ -20,9 +21,9 @@ def silu_and_mul_per_token_quant_fp8(
     x: torch.Tensor,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """``silu(x[..., :d]) * x[..., d:]`` then per-token e4m3. ``d = last_dim // 2``."""
+    if x.dtype not in _ACT:
+        raise TypeError(f"silu_and_mul_per_token_quant_fp8 takes bf16, fp16 or fp32, got {x.dtype}")
     require_device(x)
-    if x.dtype not in (torch.bfloat16, torch.float16):
-        raise TypeError(f"silu_and_mul_per_token_quant_fp8 takes bf16 or fp16, got {x.dtype}")
     last = int(x.shape[-1])
     if last % 2 != 0:
         raise ValueError("silu_and_mul_per_token_quant_fp8 needs an even last dimension")

@@ -1,5 +1,7 @@
-"""Paged KV pool: a drop-in for ``flashrec.kvcache.pool.TokenToKVPool``
-(python/flashrec/kvcache/pool.py:66-145).
+"""Paged KV pool and request-slot pool: drop-ins for
+``flashrec.kvcache.pool.TokenToKVPool`` (python/flashrec/kvcache/pool.py:66-145)
+and ``ReqToTokenPool`` (pool.py:148-182), so the module can replace the
+reference's whole ``flashrec.kvcache.pool``.
 
 Interface kept: ``TokenToKVPool(num_layers, num_tokens, num_kv_heads,
 head_dim, dtype, device)`` with per-layer ``k`` / ``v`` lists of
@@ -9,6 +11,10 @@ head_dim, dtype, device)`` with per-layer ``k`` / ``v`` lists of
 k, v, loc)``, ``k_cache(layer)``, ``v_cache(layer)`` and ``last_alloc_cpu``.
 Slot 0 is the padding slot that graph-captured batches point their unused
 rows at, so it is never handed out and freeing it is a no-op.
+``ReqToTokenPool(max_reqs, max_seq_len, device)`` keeps the int32
+``req_to_token`` table ``[max_reqs, max_seq_len]`` and hands out request rows
+1 .. max_reqs-1 with the same ``available_size`` / ``alloc`` / ``free`` /
+``last_alloc_cpu`` contract (row 0 is the dummy row pointing at KV slot 0).
 
 Design here:
 
@@ -94,7 +100,82 @@ class _PinnedUpload:
         return out
 
 
-class TokenToKVPool:
+class _FreeStack:
+    """Host-side LIFO of free ids ``1 .. n-1`` (0 is the padding id): ``take``
+    pops the top ``k`` ids in stack order (the reference's ``free[-k:]``),
+    ``give`` pushes ids back in the order given."""
+
+    def __init__(self, n: int):
+        self._stack = np.arange(1, int(n), dtype=np.int64)
+        self._top = self._stack.size
+
+    def __len__(self) -> int:
+        return self._top
+
+    def take(self, k: int) -> np.ndarray:
+        taken = self._stack[self._top - k:self._top].copy()
+        self._top -= k
+        return taken
+
+    def give(self, ids: np.ndarray) -> None:
+        need = self._top + ids.size
+        if need > self._stack.size:
+            grown = np.empty(max(need, 2 * self._stack.size), dtype=np.int64)
+            grown[:self._top] = self._stack[:self._top]
+            self._stack = grown
+        self._stack[self._top:need] = ids
+        self._top = need
+
+
+class _IdAllocator:
+    """``available_size`` / ``alloc`` / ``free`` / ``last_alloc_cpu`` over a
+    ``_FreeStack``, ids uploaded through ``_PinnedUpload`` (shared by both
+    pools: the reference's two pools have the same allocation contract,
+    pool.py:100-119 and :160-182)."""
+
+    def _init_ids(self, n: int, device: torch.device) -> None:
+        self._free_ids = _FreeStack(n)
+        self._upload = _PinnedUpload(device)
+        self.last_alloc_cpu: List[int] = []
+
+    def available_size(self) -> int:
+        return len(self._free_ids)
+
+    def alloc(self, n: int) -> Optional[torch.Tensor]:
+        """``n`` free ids on the pool's device, or ``None`` if fewer are free."""
+        n = int(n)
+        if n > len(self._free_ids):
+            self.last_alloc_cpu = []
+            return None
+        if n <= 0:
+            self.last_alloc_cpu = []
+            return torch.empty(0, dtype=torch.int64, device=self.device)
+        taken = self._free_ids.take(n)
+        self.last_alloc_cpu = taken.tolist()
+        return self._upload(taken)
+
+    def free(self, indices: Optional[Union[torch.Tensor, Sequence[int]]]) -> None:
+        """Return ids to the pool (the padding id 0 and negative ids are ignored)."""
+        ids = _host_ids(indices)
+        ids = ids[ids > 0]
+        if ids.size:
+            self._free_ids.give(ids)
+
+
+class ReqToTokenPool(_IdAllocator):
+    """Request rows of the ``req_to_token`` table (int32 KV slot ids per
+    request position); row 0 is the dummy row (python/flashrec/kvcache/pool.py:148-182)."""
+
+    def __init__(self, max_reqs: int, max_seq_len: int, device: torch.device):
+        self.max_reqs = int(max_reqs)
+        self.max_seq_len = int(max_seq_len)
+        self.device = torch.device(device)
+        self.req_to_token = torch.zeros((self.max_reqs, self.max_seq_len), dtype=torch.int32,
+                                        device=self.device)
+        self._init_ids(self.max_reqs, self.device)
+
+
+class TokenToKVPool(_IdAllocator):
     """Per-layer K and V pages ``[num_tokens, num_kv_heads, head_dim]``; slot 0 is padding."""
 
     def __init__(self, num_layers: int, num_tokens: int, num_kv_heads: int, head_dim: int,
@@ -116,42 +197,7 @@ class TokenToKVPool:
         for _ in range(self.num_layers):
             self.k.append(torch.zeros(page_shape, dtype=dtype, device=self.device))
             self.v.append(torch.zeros(page_shape, dtype=dtype, device=self.device))
-        # free stack: ids 1 .. num_tokens-1, popped from the top
-        self._stack = np.arange(1, self.num_tokens, dtype=np.int64)
-        self._top = self._stack.size
-        self._upload = _PinnedUpload(self.device)
-        self.last_alloc_cpu: List[int] = []
-
-    def available_size(self) -> int:
-        return self._top
-
-    def alloc(self, n: int) -> Optional[torch.Tensor]:
-        """``n`` free slot ids on the pool's device, or ``None`` if fewer are free."""
-        n = int(n)
-        if n > self._top:
-            self.last_alloc_cpu = []
-            return None
-        if n <= 0:
-            self.last_alloc_cpu = []
-            return torch.empty(0, dtype=torch.int64, device=self.device)
-        taken = self._stack[self._top - n:self._top].copy()
-        self._top -= n
-        self.last_alloc_cpu = taken.tolist()
-        return self._upload(taken)
-
-    def free(self, indices: Optional[Union[torch.Tensor, Sequence[int]]]) -> None:
-        """Return slots to the pool (the padding slot 0 and negative ids are ignored)."""
-        ids = _host_ids(indices)
-        ids = ids[ids > 0]
-        if ids.size == 0:
-            return
-        need = self._top + ids.size
-        if need > self._stack.size:
-            grown = np.empty(max(need, 2 * self._stack.size), dtype=np.int64)
-            grown[:self._top] = self._stack[:self._top]
-            self._stack = grown
-        self._stack[self._top:need] = ids
-        self._top = need
+        self._init_ids(self.num_tokens, self.device)
 
     def store(self, layer_id: int, k: torch.Tensor, v: torch.Tensor, loc: torch.Tensor) -> None:
         """``k_cache[loc] = k``, ``v_cache[loc] = v`` in the pool's dtype (pool.py:121-139)."""

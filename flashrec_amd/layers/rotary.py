@@ -12,7 +12,7 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 
-from flashrec_amd.kernel.sglops import apply_rope_inplace
+from flashrec_amd.kernel.sglops import apply_rope_inplace, rope_inplace_any
 
 
 def build_cos_sin_cache(head_dim: int, max_position: int, base: float) -> torch.Tensor:
@@ -34,5 +34,5 @@ class RotaryEmbedding(nn.Module):
     def forward(self, positions: torch.Tensor, query: torch.Tensor, key: torch.Tensor):
         """In-place RoPE of query [T, Hq*D] / key [T, Hk*D]; returns (query, key)."""
         if not apply_rope_inplace(positions, query, key, self.head_dim, self.cos_sin_cache):
-            raise ValueError("RoPE kernel does not take this layout (bf16, D <= 128 even, unit inner stride)")
+            rope_inplace_any(positions, query, key, self.head_dim, self.cos_sin_cache)
         return query, key

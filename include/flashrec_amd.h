@@ -49,8 +49,8 @@ int fr_quantize_weight_fp8(const void* w, int w_dtype, int64_t N, int64_t K, int
 
 /* RMSNorm (optionally after `residual += x`, residual updated in place)
  * fused with per-token e4m3 quantisation.  x, residual, w: all of x_dtype
- * (FR_DTYPE_BF16 or FR_DTYPE_FP16; intermediates rounded to it as torch
- * does); residual may be NULL.  q: [M, H] e4m3 contiguous, s: [M] fp32.
+ * (FR_DTYPE_BF16, FR_DTYPE_FP16 or FR_DTYPE_FP32; intermediates rounded to
+ * it as torch does, fp32 ones unrounded); residual may be NULL.  q: [M, H] e4m3 contiguous, s: [M] fp32.
  * Replaces python/flashrec/kernel/rms_fp8.py:120-145
  * (rmsnorm_per_token_quant_fp8, fused_add_rmsnorm_per_token_quant_fp8). */
 int fr_rms_quant_fp8(const void* x, int x_dtype, int64_t ldx, void* residual, int64_t ldr,
@@ -58,14 +58,14 @@ int fr_rms_quant_fp8(const void* x, int x_dtype, int64_t ldx, void* residual, in
 
 /* RMSNorm with x_dtype output (out may alias x); with residual != NULL it is
  * fused_add_rmsnorm: residual = round(residual + x), out = rmsnorm(residual).
- * x_dtype: FR_DTYPE_BF16 or FR_DTYPE_FP16 (x, residual, w and out).
+ * x_dtype: FR_DTYPE_BF16, FR_DTYPE_FP16 or FR_DTYPE_FP32 (x, residual, w and out).
  * Replaces python/flashrec/kernel/sglops.py:33-45 (rmsnorm) and :48-61
  * (fused_add_rmsnorm). */
 int fr_rmsnorm(const void* x, int x_dtype, int64_t ldx, void* residual, int64_t ldr,
                const void* w, void* out, int64_t ldo, int64_t M, int64_t H, float eps, void* stream);
 
-/* SiLU-and-mul over [M, 2d] rows of x_dtype (FR_DTYPE_BF16 or FR_DTYPE_FP16;
- * gate half first) fused with per-token
+/* SiLU-and-mul over [M, 2d] rows of x_dtype (FR_DTYPE_BF16, FR_DTYPE_FP16 or
+ * FR_DTYPE_FP32; gate half first) fused with per-token
  * e4m3 quantisation: q [M, d] e4m3 contiguous, s [M] fp32.
  * Replaces python/flashrec/kernel/silu_fp8.py:85-119
  * (silu_and_mul_per_token_quant_fp8). */
@@ -151,6 +151,17 @@ int fr_qk_norm_rope_store_fp8(void* q, int64_t sqt, int64_t sqh, const void* k, 
 int fr_rope_inplace(void* q, int64_t sqt, int64_t sqh, void* k, int64_t skt, int64_t skh,
                     const int64_t* positions, const float* cos_sin_cache, int64_t cache_rows,
                     int64_t T, int64_t Hq, int64_t Hk, int64_t D, void* stream);
+
+/* NeoX rotate-half RoPE in place for the layouts fr_rope_inplace does not
+ * take: q [T, Hq, D] / k [T, Hk, D] of dtype (FR_DTYPE_BF16, FR_DTYPE_FP16
+ * or FR_DTYPE_FP32) with element strides (token, head, dim), any even D.
+ * y1 = x1*cos - x2*sin, y2 = x2*cos + x1*sin in fp32, rounded once to the
+ * dtype; tokens whose position has no cache row are left as they are.
+ * Replaces the torch branch of python/flashrec/layers/rotary.py:55-71
+ * (RotaryEmbedding.forward when neither fused backend takes the layout). */
+int fr_rope_inplace_any(void* q, int64_t sqt, int64_t sqh, int64_t sqd, void* k, int64_t skt, int64_t skh,
+                        int64_t skd, int dtype, const int64_t* positions, const float* cos_sin_cache,
+                        int64_t cache_rows, int64_t T, int64_t Hq, int64_t Hk, int64_t D, void* stream);
 
 /* KV store: k/v rows [T, row_dim] (bf16 -> e4m3 with torch conversion
  * semantics, or e4m3 copied as bytes) scattered to k_cache/v_cache rows

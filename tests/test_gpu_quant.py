@@ -249,3 +249,73 @@ def test_fp16_silu_quant(dev, m, two_d):
     y = silu_and_mul(x.to(dev))
     assert y.dtype == torch.float16
     assert_bf16_parity(y, ops.silu_and_mul(x))
+
+
+@pytest.mark.parametrize("m,h", [(512, 2048), (7, 100)])
+def test_fp32_rms_quant_and_residual(dev, m, h):
+    """fp32 activations (the reference's fused op takes any x.dtype,
+    rms_fp8.py:84-86; its CPU composition keeps fp32 rows unrounded)."""
+    from flashrec_amd.kernel.rms_fp8 import (fused_add_rmsnorm_per_token_quant_fp8,
+                                             rmsnorm_per_token_quant_fp8)
+    from flashrec_amd.kernel.sglops import fused_add_rmsnorm, rmsnorm
+
+    g = torch.Generator().manual_seed(7 * m + h)
+    x = torch.randn(m, h, generator=g)
+    r = torch.randn(m, h, generator=g)
+    w = (1.0 + 0.1 * torch.randn(h, generator=g)).to(torch.bfloat16)
+    q, s = rmsnorm_per_token_quant_fp8(x.to(dev), w.to(dev), 1e-6)
+    q_ref, s_ref = ops.rmsnorm_per_token_quant_fp8(x, w, 1e-6)
+    assert_fp8_parity(q, s, q_ref, s_ref, label=f"fp32 rms {m}x{h}")
+    rd = r.to(dev)
+    q, s, res = fused_add_rmsnorm_per_token_quant_fp8(x.to(dev), rd, w.to(dev), 1e-6)
+    q_ref, s_ref, res_ref = ops.fused_add_rmsnorm_per_token_quant_fp8(x, r, w, 1e-6)
+    assert res.dtype == torch.float32 and torch.equal(res.cpu(), res_ref)  # one fp32 add: exact
+    assert_fp8_parity(q, s, q_ref, s_ref, label=f"fp32 add+rms {m}x{h}")
+    # unquantized fp32 outputs: only the variance's summation order differs,
+    # which moves rsqrt by a few fp32 ulps
+    y = rmsnorm(x.to(dev), w.to(dev), 1e-6)
+    assert y.dtype == torch.float32
+    torch.testing.assert_close(y.cpu(), ops.rmsnorm(x, w, 1e-6), rtol=4e-6, atol=0)
+    xd, rd = x.to(dev), r.to(dev)
+    y, res = fused_add_rmsnorm(xd, rd, w.to(dev), 1e-6)
+    y_ref, res_ref = ops.fused_add_rmsnorm(x, r, w, 1e-6)
+    assert torch.equal(res.cpu(), res_ref)
+    torch.testing.assert_close(y.cpu(), y_ref, rtol=4e-6, atol=0)
+
+
+@pytest.mark.parametrize("m,two_d", [(64, 12288), (5, 100)])
+def test_fp32_silu_quant(dev, m, two_d):
+    from flashrec_amd.kernel.sglops import silu_and_mul
+    from flashrec_amd.kernel.silu_fp8 import silu_and_mul_per_token_quant_fp8
+
+    g = torch.Generator().manual_seed(two_d + 1)
+    x = 3 * torch.randn(m, two_d, generator=g)
+    q, s = silu_and_mul_per_token_quant_fp8(x.to(dev))
+    q_ref, s_ref = ops.silu_and_mul_per_token_quant_fp8(x)
+    assert_fp8_parity(q, s, q_ref, s_ref, label=f"fp32 silu {m}x{two_d}")
+    # fp32 outputs: exp differs from torch's vectorised CPU exp by an ulp or so
+    y = silu_and_mul(x.to(dev))
+    assert y.dtype == torch.float32
+    torch.testing.assert_close(y.cpu(), ops.silu_and_mul(x), rtol=4e-6, atol=1e-30)
+
+
+def test_silu_unaligned_rows_match_aligned(dev):
+    """A row that the vector kernel takes and the same row through the generic
+    kernel (a strided, unaligned view) give the same bits: both use one SiLU
+    arithmetic."""
+    from flashrec_amd.kernel.sglops import silu_and_mul
+    from flashrec_amd.kernel.silu_fp8 import silu_and_mul_per_token_quant_fp8
+
+    g = torch.Generator().manual_seed(11)
+    x = (4 * torch.randn(96, 2048, generator=g)).to(torch.bfloat16)
+    x[3, 5] = 100.0  # a gate beyond the in-range form in one row
+    aligned = x.to(dev)
+    holder = torch.zeros(96, 2048 + 1, dtype=torch.bfloat16, device=dev)
+    holder[:, 1:] = aligned
+    unaligned = holder[:, 1:]  # rows start 2 bytes into a 16-byte line
+    assert unaligned.data_ptr() % 16 != 0
+    assert torch.equal(silu_and_mul(unaligned).cpu().view(torch.int16),
+                       silu_and_mul(aligned).cpu().view(torch.int16))
+    qa, sa = silu_and_mul_per_token_quant_fp8(aligned)
+    qu, su = silu_and_mul_per_token_quant_fp8(unaligned)
+    assert torch.equal(codes(qa), codes(qu)) and torch.equal(sa.cpu(), su.cpu())

@@ -255,3 +255,75 @@ def test_store_kv_cache_bf16_pool(dev):
     ref3 = torch.zeros(slots, 37, dtype=torch.bfloat16)
     ref3[loc] = k3
     assert torch.equal(kc3.cpu(), ref3) and torch.equal(vc3.cpu(), ref3)
+
+
+@pytest.mark.parametrize("dtype,d,strided", [(torch.float16, 128, False), (torch.float32, 128, False),
+                                             (torch.bfloat16, 256, False), (torch.bfloat16, 64, True),
+                                             (torch.float32, 192, True)])
+def test_rotary_embedding_other_layouts(dev, dtype, d, strided):
+    """RotaryEmbedding.forward answers for the layouts the bf16 kernel declines
+    (the reference falls through to FlashInfer or torch there,
+    python/flashrec/layers/rotary.py:43-71): fp16 / fp32 heads, D > 128 and
+    heads whose elements are not contiguous, bit-exact with the oracle."""
+    from flashrec_amd.layers.rotary import RotaryEmbedding
+
+    t, hq, hk = 37, 4, 2
+    g = torch.Generator().manual_seed(d + (7 if strided else 0))
+    q = torch.randn(t, hq * d, generator=g).to(dtype)
+    k = torch.randn(t, hk * d, generator=g).to(dtype)
+    rope = RotaryEmbedding(d, 512, 1e6, device=dev)
+    pos = torch.randint(0, 512, (t,), generator=g)
+    if strided:  # every other element of a wider buffer
+        qb = torch.zeros(t, 2 * hq * d, dtype=dtype, device=dev)
+        kb = torch.zeros(t, 2 * hk * d, dtype=dtype, device=dev)
+        qd, kd = qb[:, ::2], kb[:, ::2]
+        qd.copy_(q.to(dev))
+        kd.copy_(k.to(dev))
+    else:
+        qd, kd = q.to(dev), k.to(dev)
+    qo, ko = rope(pos.to(dev), qd, kd)
+    assert qo.data_ptr() == qd.data_ptr() and ko.data_ptr() == kd.data_ptr()
+    cache = ops.cos_sin_cache(d, 512, 1e6)
+    q_ref = ops.apply_rope(pos, q.view(t, hq, d), cache).reshape(t, -1)
+    k_ref = ops.apply_rope(pos, k.view(t, hk, d), cache).reshape(t, -1)
+    assert torch.equal(qd.cpu(), q_ref) and torch.equal(kd.cpu(), k_ref)
+    if strided:  # the interleaved elements are untouched
+        assert not qb[:, 1::2].any() and not kb[:, 1::2].any()
+
+
+def test_out_of_range_position_writes_no_kv(dev):
+    """A token whose position has no cos/sin row leaves its slot as it was:
+    neither K nor V is written (fp8 pool through the fused op, bf16 pool
+    through apply_rope_and_store_kv)."""
+    from flashrec_amd.kernel.qk_rope_kv import fused_qk_norm_rope_store_fp8
+    from flashrec_amd.kernel.sglops import apply_rope_and_store_kv
+
+    t, hq, hk, d, slots, rows = 16, 16, 8, 128, 64, 256
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(t, hq, d, generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn(t, hk, d, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(t, hk, d, generator=g).to(torch.bfloat16).to(dev)
+    pos = torch.randint(0, rows, (t,), generator=g)
+    pos[3] = rows + 5
+    pos[9] = -1
+    loc = (torch.randperm(slots - 1, generator=g)[:t] + 1).to(dev)
+    cache = ops.cos_sin_cache(d, rows, 1e6).to(dev)
+    w = torch.ones(d, dtype=torch.bfloat16, device=dev)
+    kc = torch.zeros(slots, hk, d, dtype=torch.float8_e4m3fn, device=dev)
+    vc = torch.zeros_like(kc)
+    assert fused_qk_norm_rope_store_fp8(q.clone(), k, v, pos.to(dev), loc, w, w, 1e-6, cache, kc, vc)
+    for cache_k, cache_v in ((kc, vc),):
+        for bad in (3, 9):
+            s = int(loc[bad])
+            assert not codes(cache_k[s]).any() and not codes(cache_v[s]).any()
+        good = [i for i in range(t) if i not in (3, 9)]
+        assert codes(cache_v[loc[good]]).any()
+    kb = torch.zeros(slots, hk * d, dtype=torch.bfloat16, device=dev)
+    vb = torch.zeros_like(kb)
+    assert apply_rope_and_store_kv(pos.to(dev), q.clone().view(t, -1), k.clone().view(t, -1),
+                                   v.view(t, -1), loc, kb, vb, d, cache)
+    for bad in (3, 9):
+        s = int(loc[bad])
+        assert not kb[s].any() and not vb[s].any()
+    good = [i for i in range(t) if i not in (3, 9)]
+    assert torch.equal(vb[loc[good]], v[good].reshape(len(good), -1))

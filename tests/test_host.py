@@ -222,3 +222,62 @@ def test_pinned_upload_ring_reuses_regions():
     assert start == 0 and evs[0].waited and not evs[1].waited and not evs[2].waited
     start = up._reserve(4)  # [5, 9) meets (6, 12)
     assert start == 5 and evs[1].waited and not evs[2].waited
+
+
+def test_req_to_token_pool_contract():
+    """ReqToTokenPool (python/flashrec/kvcache/pool.py:148-182): an int32
+    [max_reqs, max_seq_len] table, row 0 never handed out, rows taken from
+    the top of the free list and returned in order."""
+    from flashrec_amd.kvcache import ReqToTokenPool
+
+    pool = ReqToTokenPool(6, 32, torch.device("cpu"))
+    assert pool.req_to_token.shape == (6, 32) and pool.req_to_token.dtype == torch.int32
+    assert not pool.req_to_token.any()
+    assert pool.available_size() == 5
+    got = pool.alloc(2)
+    assert got.dtype == torch.int64 and got.tolist() == [4, 5] and pool.last_alloc_cpu == [4, 5]
+    assert pool.alloc(4) is None and pool.last_alloc_cpu == []
+    assert pool.alloc(0).numel() == 0
+    pool.free(torch.tensor([0, 5, -1]))
+    assert pool.available_size() == 4
+    assert pool.alloc(1).tolist() == [5]
+    assert sorted(pool.alloc(3).tolist()) == [1, 2, 3] and pool.available_size() == 0
+
+
+def test_kvcache_module_exports_both_pools():
+    import flashrec_amd.kvcache as kv
+    from flashrec_amd.kvcache import pool
+
+    assert kv.ReqToTokenPool is pool.ReqToTokenPool and kv.TokenToKVPool is pool.TokenToKVPool
+
+
+def test_row_kernels_refuse_other_dtypes_before_launch():
+    """bf16, fp16 and fp32 activations are taken (fp32 without intermediate
+    rounding, as the reference's CPU composition); other dtypes raise
+    TypeError before any device work, and host tensors of a taken dtype raise
+    the no-CPU-path error (there is no fallback)."""
+    from flashrec_amd.kernel.rms_fp8 import (fused_add_rmsnorm_per_token_quant_fp8,
+                                             rmsnorm_per_token_quant_fp8)
+    from flashrec_amd.kernel.silu_fp8 import silu_and_mul_per_token_quant_fp8
+
+    w = torch.ones(8, dtype=torch.bfloat16)
+    x64 = torch.ones(2, 8, dtype=torch.float64)
+    with pytest.raises(TypeError):
+        rmsnorm_per_token_quant_fp8(x64, w, 1e-6)
+    with pytest.raises(TypeError):
+        fused_add_rmsnorm_per_token_quant_fp8(torch.ones(2, 8), torch.ones(2, 8, dtype=torch.bfloat16), w, 1e-6)
+    with pytest.raises(TypeError):
+        silu_and_mul_per_token_quant_fp8(x64)
+    for dt in (torch.bfloat16, torch.float16, torch.float32):
+        with pytest.raises(RuntimeError, match="no CPU path"):
+            rmsnorm_per_token_quant_fp8(torch.ones(2, 8, dtype=dt), w, 1e-6)
+        with pytest.raises(RuntimeError, match="no CPU path"):
+            silu_and_mul_per_token_quant_fp8(torch.ones(2, 8, dtype=dt))
+
+
+def test_rotary_embedding_refuses_odd_head():
+    from flashrec_amd.kernel.sglops import rope_inplace_any
+
+    with pytest.raises((ValueError, RuntimeError)):
+        rope_inplace_any(torch.zeros(2, dtype=torch.int64), torch.zeros(2, 6), torch.zeros(2, 6), 3,
+                         torch.zeros(4, 3))
