@@ -49,6 +49,10 @@ SIGNATURES = {
     "fr_fp8_scaled_mm_residual": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64,
                                   _I32, _P],
     "fr_fp8_scaled_mm_silu": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P],
+    "fr_fp8_weight_prearranged_bytes": [_I64, _I64],
+    "fr_fp8_weight_prearrange": [_P, _I64, _I64, _I64, _P, _P],
+    "fr_fp8_scaled_mm_prearranged": [_P, _I64, _P, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I32,
+                                     _I32, _P],
     "fr_qk_norm_rope_store_fp8": [
         _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,  # q, k, v + strides
         _P, _P, _P, _P, _F32, _P, _I64,  # pos, loc, qw, kw, eps, cos_sin, rows
@@ -134,6 +138,7 @@ def load() -> ctypes.CDLL:
         fn.argtypes = argtypes
         fn.restype = ctypes.c_int
     lib.fr_paged_attention_plan_size.restype = ctypes.c_int64
+    lib.fr_fp8_weight_prearranged_bytes.restype = ctypes.c_int64
     _LIB = lib
     return lib
 

@@ -66,11 +66,18 @@ __device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
 // fp32 rows keep them unrounded); the residual, the norm weight and the
 // unquantized output rows are in that dtype too.
 //
-// SiLU: the same arithmetic as the vector kernel and the GEMM's SiLU
-// epilogue (silu_in_range for |g| <= 80, torch's formula beyond), so a row
-// gives the same bits whichever kernel takes it.
+// SiLU of bf16 rows: the same arithmetic as the vector kernel and the GEMM's
+// SiLU epilogue (silu_in_range for |g| <= 80, torch's formula beyond), so a
+// bf16 row gives the same bits whichever kernel takes it (aligned or not,
+// GEMM epilogue or row kernel).  fp16 and fp32 rows only ever take this
+// kernel and keep torch's formula: their finer roundings (fp16 subnormals,
+// unrounded fp32) show the last-ulp differences of the in-range form.
+template <int DT>
 __device__ __forceinline__ float silu_any(float g) {
-  return __builtin_fabsf(g) <= 80.0f ? silu_in_range(g) : g / (1.0f + expf(-g));
+  if constexpr (DT == FR_DTYPE_BF16)
+    return __builtin_fabsf(g) <= 80.0f ? silu_in_range(g) : g / (1.0f + expf(-g));
+  else
+    return g / (1.0f + expf(-g));
 }
 
 template <int MODE, int DT, bool QOUT>
@@ -106,7 +113,7 @@ __device__ __forceinline__ void generic_row(const RowArgs& a, int64_t row, int l
     } else {
       val = E::load(xr + e);
     }
-    if (MODE == kSilu) val = H::round(H::round(silu_any(val)) * E::load(xr + K + e));
+    if (MODE == kSilu) val = H::round(H::round(silu_any<DT>(val)) * E::load(xr + K + e));
     if (MODE == kRms || MODE == kAddRms) val = H::round((val * rstd) * H::load(wr + e));
     return val;
   };

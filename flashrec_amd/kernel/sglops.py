@@ -9,11 +9,11 @@ missing or broken native library).
 
 from __future__ import annotations
 
-from typing import Optional
+from typing import NamedTuple, Optional
 
 import torch
 
-from flashrec_amd._lib import DTYPE_CODE, call, ptr, require_device, stream_of
+from flashrec_amd._lib import DTYPE_CODE, call, load, ptr, require_device, stream_of
 
 _FP8_MAX = 448.0
 
@@ -260,6 +260,100 @@ def fp8_scaled_mm_residual(
     return out
 
 
+class PrearrangedFp8Weight(NamedTuple):
+    """e4m3 weight codes of an ``[N, K]`` matrix rearranged once for
+    ``fp8_scaled_mm_prearranged``: blocks of 32 rows x 64 bytes of K, each
+    stored in the order a wave's MFMA operand registers hold it, so the GEMM
+    loads weights as contiguous 1 KB runs straight into registers."""
+
+    data: torch.Tensor  # uint8 [fr_fp8_weight_prearranged_bytes(N, K)]
+    n: int
+    k: int
+
+
+def prearrange_fp8_weight(b_fp8: torch.Tensor) -> PrearrangedFp8Weight:
+    """``b_fp8``: the ``[K, N]`` e4m3 weight of ``fp8_scaled_mm`` (any strides;
+    ``Linear`` keeps it as the column-major view of ``[N, K]`` codes).  A new
+    buffer; the codes are copied bit for bit."""
+    if b_fp8.dtype != torch.float8_e4m3fn or b_fp8.dim() != 2:
+        raise TypeError("prearrange_fp8_weight takes a 2-D float8_e4m3fn [K, N] weight")
+    require_device(b_fp8)
+    k, n = int(b_fp8.shape[0]), int(b_fp8.shape[1])
+    rows = b_fp8.t()
+    if not (rows.stride(1) == 1 and (n <= 1 or rows.stride(0) >= k)):
+        rows = rows.contiguous()
+    nbytes = int(load().fr_fp8_weight_prearranged_bytes(n, k))
+    if nbytes < 0:
+        raise ValueError(f"cannot prearrange a [{n}, {k}] weight")
+    data = torch.empty(nbytes, dtype=torch.uint8, device=b_fp8.device)
+    if nbytes:
+        call("fr_fp8_weight_prearrange", rows.data_ptr(), rows.stride(0) if n > 1 else k, n, k, data.data_ptr(),
+             stream_of(b_fp8))
+    return PrearrangedFp8Weight(data, n, k)
+
+
+@torch.compiler.disable
+def fp8_scaled_mm_prearranged(
+    a_fp8: torch.Tensor,
+    w: PrearrangedFp8Weight,
+    scale_a: torch.Tensor,
+    scale_b: torch.Tensor,
+    out_dtype: torch.dtype = torch.bfloat16,
+    residual: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
+    silu: bool = False,
+) -> torch.Tensor:
+    """``fp8_scaled_mm(a, b, scale_a, scale_b, out_dtype)`` with ``b`` given
+    as ``prearrange_fp8_weight(b)``: the same results bit for bit.  With
+    ``residual`` the product (rounded to the residual's dtype) is added into
+    it, as ``fp8_scaled_mm_residual`` (``out`` defaults to the residual);
+    with ``silu`` the weight must be gate/up interleaved (``interleave_gate_up``)
+    and the output is ``[M, N / 2]`` bf16, as ``fp8_scaled_mm_silu``."""
+    if a_fp8.dtype != torch.float8_e4m3fn or a_fp8.dim() != 2:
+        raise TypeError("fp8_scaled_mm_prearranged takes a 2-D float8_e4m3fn activation")
+    m, k = int(a_fp8.shape[0]), int(a_fp8.shape[1])
+    n = w.n
+    if k != w.k:
+        raise ValueError(f"activation K {k} does not match the weight's {w.k}")
+    if silu:
+        if residual is not None or n % 16:
+            raise ValueError("the SiLU form takes no residual and N a multiple of 16")
+        out_dtype = torch.bfloat16
+    if residual is not None:
+        if residual.dtype not in _HALF or tuple(residual.shape) != (m, n) or residual.stride(1) != 1:
+            raise ValueError(f"residual must be bf16/fp16 [{m}, {n}] with a unit inner stride")
+        out_dtype = residual.dtype
+        if out is None:
+            out = residual
+    if out_dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise TypeError(f"unsupported out_dtype {out_dtype}")
+    n_out = n // 2 if silu else n
+    if out is None:
+        out = torch.empty((m, n_out), dtype=out_dtype, device=a_fp8.device)
+    if out.dtype != out_dtype or tuple(out.shape) != (m, n_out) or out.stride(1) != 1:
+        raise ValueError(f"out must be {out_dtype} [{m}, {n_out}] with a unit inner stride")
+    require_device(a_fp8, w.data, out)
+    a = a_fp8 if a_fp8.stride(1) == 1 and (m <= 1 or a_fp8.stride(0) >= k) else a_fp8.contiguous()
+    lda = a.stride(0) if m > 1 else k
+    if k % 16 or lda % 16 or a.data_ptr() % 16:
+        # the activation ring takes 16-byte rows: zero-pad K (the weight's
+        # prearranged K steps already hold zeros there)
+        k16 = (k + 15) // 16 * 16
+        a16 = torch.zeros((m, k16), dtype=torch.uint8, device=a.device)
+        a16[:, :k] = a.view(torch.uint8)
+        a, k, lda = a16.view(a_fp8.dtype), k16, k16
+    sa = scale_a.reshape(-1).to(device=a.device, dtype=torch.float32).contiguous()
+    sb = scale_b.reshape(-1).to(device=a.device, dtype=torch.float32).contiguous()
+    if sa.numel() not in (1, m) or sb.numel() not in (1, n):
+        raise ValueError("scale_a must have 1 or M values and scale_b 1 or N values")
+    ldr = 0 if residual is None else (residual.stride(0) if m > 1 else n)
+    ldo = out.stride(0) if m > 1 else n_out
+    call("fr_fp8_scaled_mm_prearranged", a.data_ptr(), lda, w.data.data_ptr(), sa.data_ptr(), sa.numel(),
+         sb.data_ptr(), sb.numel(), ptr(residual), ldr, out.data_ptr(), ldo, m, n, k, DTYPE_CODE[out_dtype],
+         int(silu), stream_of(a))
+    return out
+
+
 def interleave_gate_up(t: torch.Tensor, dim: int = 0) -> torch.Tensor:
     """The gate half then the up half of ``t`` along ``dim`` (2n entries, n a
     multiple of 8) reordered into chunks of 16: 8 gate entries followed by
@@ -464,6 +558,9 @@ __all__ = [
     "per_token_quant_fp8",
     "fp8_scaled_mm",
     "fp8_scaled_mm_silu",
+    "prearrange_fp8_weight",
+    "fp8_scaled_mm_prearranged",
+    "PrearrangedFp8Weight",
     "interleave_gate_up",
     "silu_and_mul",
     "apply_rope_and_store_kv",

@@ -126,6 +126,33 @@ int fr_fp8_scaled_mm_silu(const void* a, int64_t lda, const void* b, int64_t ldb
                           int64_t scale_a_numel, const float* scale_b, int64_t scale_b_numel, void* out,
                           int64_t ldo, int64_t M, int64_t N, int64_t K, void* stream);
 
+/* Weights rearranged once for the prearranged GEMM below: the [N, K] e4m3
+ * rows w (row stride ldw bytes) as blocks of 32 rows x 64 bytes of K, each
+ * block the two 1 KB halves a wave's MFMA operand registers hold:
+ *   out[((n/32)*KT + k/64)*2048 + h*1024 + l*16 + b]
+ *     = w[32*(n/32) + l%32][64*(k/64) + 32*(l/32) + 16*h + b]
+ * (KT = ceil(K / 64) rounded up to a multiple of 4; rows past N and bytes
+ * past K are zero).  out holds fr_fp8_weight_prearranged_bytes(N, K) bytes,
+ * 16-byte aligned.  A layout step of the weight-load path (the reference
+ * keeps weights as [K, N] column-major views, python/flashrec/layers/
+ * linear.py:104-109); it has no counterpart of its own in the reference. */
+int64_t fr_fp8_weight_prearranged_bytes(int64_t N, int64_t K);
+int fr_fp8_weight_prearrange(const void* w, int64_t ldw, int64_t N, int64_t K, void* out, void* stream);
+
+/* fr_fp8_scaled_mm with the weight given prearranged (w_pre, for this N and
+ * K): the same results bit for bit, the weights streamed as contiguous
+ * 1 KB runs straight into registers.  residual (bf16/fp16 out_dtype, [M, N],
+ * row stride ldr, may alias out) or NULL: as fr_fp8_scaled_mm_residual.
+ * silu != 0: as fr_fp8_scaled_mm_silu (bf16, N a multiple of 16, gate/up
+ * interleaved weight rows, out [M, N/2]).  No bias.  a: K a multiple of 16,
+ * lda a multiple of 16, 16-byte aligned (else FR_EUNSUPPORTED).
+ * Replaces python/flashrec/kernel/sglops.py:99-140 (fp8_scaled_mm) for
+ * weights the Linear layer owns. */
+int fr_fp8_scaled_mm_prearranged(const void* a, int64_t lda, const void* w_pre, const float* scale_a,
+                                 int64_t scale_a_numel, const float* scale_b, int64_t scale_b_numel,
+                                 const void* residual, int64_t ldr, void* out, int64_t ldo, int64_t M, int64_t N,
+                                 int64_t K, int out_dtype, int silu, void* stream);
+
 /* Per-head RMSNorm of q and k (weights q_weight, k_weight: bf16 [D]),
  * NeoX rotate-half RoPE from cos_sin_cache ([cache_rows, D] fp32: cos for
  * i < D/2, sin after), q rotated in place (bf16), rotated k and raw v

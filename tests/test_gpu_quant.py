@@ -7,7 +7,7 @@ outputs are compared with ``oracle.ops`` (the reference's CPU arithmetic).
 import pytest
 import torch
 
-from helpers import assert_bf16_parity, assert_fp8_parity, codes
+from helpers import assert_bf16_parity, assert_fp8_parity, code_flip_stats, codes
 from oracle import inputs, ops
 
 pytestmark = pytest.mark.gpu
@@ -251,6 +251,18 @@ def test_fp16_silu_quant(dev, m, two_d):
     assert_bf16_parity(y, ops.silu_and_mul(x))
 
 
+def _assert_fp32_row_parity(q, s, q_ref, s_ref, label):
+    """fp32 activations: the rows are never rounded to 16 bits, so a different
+    fp32 summation order (the RMS variance) or exp moves amax, and with it the
+    scale, by a few fp32 ulps on many rows; the bar is then scales within
+    1e-6 relative and codes equal but for 1-ULP flips on < 0.1 % of elements."""
+    s, s_ref = s.detach().cpu().reshape(-1), s_ref.reshape(-1)
+    rel = ((s - s_ref).abs() / s_ref.abs()).max().item()
+    frac, dist = code_flip_stats(q, q_ref)
+    print(f"parity {label}: scales within {rel:.2e}, {frac:.2e} of codes flipped")
+    assert rel <= 1e-6 and dist <= 1 and frac < 1e-3
+
+
 @pytest.mark.parametrize("m,h", [(512, 2048), (7, 100)])
 def test_fp32_rms_quant_and_residual(dev, m, h):
     """fp32 activations (the reference's fused op takes any x.dtype,
@@ -265,12 +277,12 @@ def test_fp32_rms_quant_and_residual(dev, m, h):
     w = (1.0 + 0.1 * torch.randn(h, generator=g)).to(torch.bfloat16)
     q, s = rmsnorm_per_token_quant_fp8(x.to(dev), w.to(dev), 1e-6)
     q_ref, s_ref = ops.rmsnorm_per_token_quant_fp8(x, w, 1e-6)
-    assert_fp8_parity(q, s, q_ref, s_ref, label=f"fp32 rms {m}x{h}")
+    _assert_fp32_row_parity(q, s, q_ref, s_ref, f"fp32 rms {m}x{h}")
     rd = r.to(dev)
     q, s, res = fused_add_rmsnorm_per_token_quant_fp8(x.to(dev), rd, w.to(dev), 1e-6)
     q_ref, s_ref, res_ref = ops.fused_add_rmsnorm_per_token_quant_fp8(x, r, w, 1e-6)
     assert res.dtype == torch.float32 and torch.equal(res.cpu(), res_ref)  # one fp32 add: exact
-    assert_fp8_parity(q, s, q_ref, s_ref, label=f"fp32 add+rms {m}x{h}")
+    _assert_fp32_row_parity(q, s, q_ref, s_ref, f"fp32 add+rms {m}x{h}")
     # unquantized fp32 outputs: only the variance's summation order differs,
     # which moves rsqrt by a few fp32 ulps
     y = rmsnorm(x.to(dev), w.to(dev), 1e-6)
@@ -292,7 +304,7 @@ def test_fp32_silu_quant(dev, m, two_d):
     x = 3 * torch.randn(m, two_d, generator=g)
     q, s = silu_and_mul_per_token_quant_fp8(x.to(dev))
     q_ref, s_ref = ops.silu_and_mul_per_token_quant_fp8(x)
-    assert_fp8_parity(q, s, q_ref, s_ref, label=f"fp32 silu {m}x{two_d}")
+    _assert_fp32_row_parity(q, s, q_ref, s_ref, f"fp32 silu {m}x{two_d}")
     # fp32 outputs: exp differs from torch's vectorised CPU exp by an ulp or so
     y = silu_and_mul(x.to(dev))
     assert y.dtype == torch.float32
