@@ -87,10 +87,11 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_pre(GemmArgs g) {
   static_assert(!SILU || OUT == FR_DTYPE_BF16, "SiLU epilogue writes bf16");
   static_assert(FN >= 1 && FM >= 1 && BN % 128 == 0 && BM % 32 == 0, "tile shape");
   static_assert(NSL >= 3, "the slot waits below assume at least three slots");
-  constexpr bool kNarrow = NSL * STAGE + 2 * 2048 + 4 * 32 * 128 > 160 * 1024 || WN % (128 / EB) != 0;
+  constexpr int kLds = 160 * 1024;
+  constexpr bool kNarrow = NSL * STAGE + 2 * 2048 + 4 * 32 * 128 > kLds || WN % (128 / EB) != 0;
   constexpr int SRB = kNarrow ? 64 : 128;
   constexpr int STG = 32 * SRB;
-  static_assert(NSL * STAGE + 2 * 2048 + 4 * STG <= 160 * 1024, "LDS");
+  static_assert(NSL * STAGE + 2 * 2048 + 4 * STG <= kLds, "LDS");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NSL * STAGE + 2 * 2048 + 4 * STG];
 
   const int tid = threadIdx.x;

@@ -160,9 +160,12 @@ class Qwen3FP8DecodeStep:
             raise ValueError("no lm_head weight (and embeddings are not tied)")
         self.weights = weights
         self.layers = weights.layers
-        # gate_up weights with gate/up rows interleaved for the SiLU-and-mul
-        # epilogue, built once here rather than inside a captured step
+        # prearranged weights (and the gate_up weights with gate/up rows
+        # interleaved for the SiLU-and-mul epilogue), built once here rather
+        # than inside a captured step
         for L in self.layers:
+            for lin in (L.qkv_proj, L.o_proj, L.down_proj):
+                lin.prepare()
             L.gate_up_proj._glu_operands()
         self.final_norm = weights.final_norm
         self.embed = weights.lm_head_weight

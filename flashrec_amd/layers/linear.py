@@ -19,6 +19,10 @@ moves them with the module (a float cast of the module leaves them as they
 are); ``_fp8_weight`` / ``_fp8_scale`` are views of them.  A call runs on the
 HIP library only: per-token e4m3 quantisation of the activations, then the
 W8A8 GEMM with both scales and the optional bias applied in its epilogue.
+Beside the codes the layer keeps them once more in the prearranged GEMM's
+layout (MFMA fragment order, built when the codes reach the GPU, about the
+codes' size again): every bias-free call runs that kernel, which gives the
+same bits as ``fp8_scaled_mm`` on the codes.
 
 Behaviour that differs from the reference on purpose: a failing fp8 GEMM
 raises instead of being retried as a dequantised bf16 ``F.linear``
@@ -34,8 +38,8 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from flashrec_amd._lib import DTYPE_CODE, call, require_device, stream_of
-from flashrec_amd.kernel.sglops import (fp8_scaled_mm, fp8_scaled_mm_residual, fp8_scaled_mm_silu,
-                                        interleave_gate_up, per_token_quant_fp8)
+from flashrec_amd.kernel.sglops import (PrearrangedFp8Weight, fp8_scaled_mm, fp8_scaled_mm_prearranged,
+                                        interleave_gate_up, per_token_quant_fp8, prearrange_fp8_weight)
 
 _E4M3 = torch.float8_e4m3fn
 _FP8_DTYPES = frozenset({torch.float8_e4m3fn, torch.float8_e5m2})
@@ -106,15 +110,31 @@ class Linear(nn.Module):
     def _fp8_scale(self) -> Optional[torch.Tensor]:
         return self.w_scale
 
+    def _prearranged(self) -> PrearrangedFp8Weight:
+        """The codes in the prearranged GEMM's layout, built when first needed
+        on the codes' device (and kept until the weights change or move)."""
+        cached = self.__dict__.get("_pre")
+        if cached is None or cached.data.device != self.w_codes.device:
+            cached = prearrange_fp8_weight(self.w_codes.t())
+            self.__dict__["_pre"] = cached
+        return cached
+
     def _glu_operands(self):
-        """The codes and scales with gate/up rows interleaved for
-        ``forward_fp8_silu``: built on first use (a copy of the codes, kept
-        until the weights change or move)."""
+        """The prearranged codes and the scales with gate/up rows interleaved
+        for ``forward_fp8_silu`` (the interleaved codes themselves are not
+        kept), built on first use."""
         cached = self.__dict__.get("_glu")
-        if cached is None or cached[0].device != self.w_codes.device:
-            cached = (interleave_gate_up(self.w_codes), interleave_gate_up(self.w_scale))
+        if cached is None or cached[0].data.device != self.w_codes.device:
+            cached = (prearrange_fp8_weight(interleave_gate_up(self.w_codes).t()), interleave_gate_up(self.w_scale))
             self.__dict__["_glu"] = cached
         return cached
+
+    def prepare(self) -> None:
+        """Build the prearranged weights now (eagerly, e.g. before a HIP graph
+        is captured), for the plain and, for gate_up projections, the
+        SiLU-and-mul forms."""
+        if self.w_codes is not None and self.w_codes.is_cuda:
+            self._prearranged()
 
     def _apply(self, fn, recurse=True):
         # Module.to() / .cuda() / .half() move the codes and scales to the new
@@ -164,6 +184,7 @@ class Linear(nn.Module):
     def _set_codes(self, codes: torch.Tensor, scale: torch.Tensor) -> None:
         # ``codes`` is the [N, K] matrix (a transposed [K, N] view stays a view)
         self.__dict__.pop("_glu", None)
+        self.__dict__.pop("_pre", None)
         self.w_codes = codes
         self.w_scale = scale.to(device=codes.device, dtype=torch.float32).reshape(self.out_features)
         self.weight = nn.Parameter(torch.empty(0, device=codes.device), requires_grad=False)
@@ -190,8 +211,11 @@ class Linear(nn.Module):
         if self.w_codes.device != q.device:
             raise ValueError(f"activations on {q.device}, fp8 weights on {self.w_codes.device}: "
                              "move the module with .to() first")
-        bias = None if self.bias is None else self.bias.to(dtype=out_dtype)
-        out = fp8_scaled_mm(q, self.w_codes.t(), a_scale, self.w_scale, out_dtype, bias)
+        if self.bias is None:
+            out = fp8_scaled_mm_prearranged(q, self._prearranged(), a_scale, self.w_scale, out_dtype)
+        else:
+            out = fp8_scaled_mm(q, self.w_codes.t(), a_scale, self.w_scale, out_dtype,
+                                self.bias.to(dtype=out_dtype))
         return out.view(*tuple(orig_shape)[:-1], self.out_features)
 
     def forward_fp8_residual(self, q: torch.Tensor, a_scale: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
@@ -207,7 +231,7 @@ class Linear(nn.Module):
         if self.w_codes.device != q.device:
             raise ValueError(f"activations on {q.device}, fp8 weights on {self.w_codes.device}: "
                              "move the module with .to() first")
-        return fp8_scaled_mm_residual(q, self.w_codes.t(), a_scale, self.w_scale, residual)
+        return fp8_scaled_mm_prearranged(q, self._prearranged(), a_scale, self.w_scale, residual=residual)
 
     def forward_fp8_silu(self, q: torch.Tensor, a_scale: torch.Tensor, out: Optional[torch.Tensor] = None
                          ) -> torch.Tensor:
@@ -222,5 +246,5 @@ class Linear(nn.Module):
         if self.w_codes.device != q.device:
             raise ValueError(f"activations on {q.device}, fp8 weights on {self.w_codes.device}: "
                              "move the module with .to() first")
-        codes, scale = self._glu_operands()
-        return fp8_scaled_mm_silu(q, codes.t(), a_scale, scale, out)
+        pre, scale = self._glu_operands()
+        return fp8_scaled_mm_prearranged(q, pre, a_scale, scale, out=out, silu=True)

@@ -33,7 +33,8 @@ from typing import List, Optional, Sequence, Tuple
 import torch
 import torch.nn.functional as F
 
-from flashrec_amd.kernel.sglops import fp8_scaled_mm, log_softmax_f32, per_token_quant_fp8
+from flashrec_amd.kernel.sglops import (PrearrangedFp8Weight, fp8_scaled_mm, fp8_scaled_mm_prearranged,
+                                        log_softmax_f32, per_token_quant_fp8, prearrange_fp8_weight)
 from flashrec_amd.layers.linear import quantize_weight_fp8
 
 
@@ -45,6 +46,7 @@ class _RowBlock:
     ids: torch.Tensor  # [n] int64, on the weight's device
     codes: Optional[torch.Tensor] = None  # [n, hidden] e4m3 (fp8 heads)
     scale: Optional[torch.Tensor] = None  # [n] fp32
+    pre: Optional[PrearrangedFp8Weight] = None  # the codes prearranged (whole heads, not level cuts)
 
     @property
     def rows(self) -> int:
@@ -65,6 +67,8 @@ class _RowBlock:
 
     def logits_fp8(self, a_codes: torch.Tensor, a_scale: torch.Tensor) -> torch.Tensor:
         """fp32 logits from hidden rows already quantised per token (fp8 heads)."""
+        if self.pre is not None:
+            return fp8_scaled_mm_prearranged(a_codes, self.pre, a_scale, self.scale, torch.float32)
         return fp8_scaled_mm(a_codes, self.codes.t(), a_scale, self.scale, torch.float32)
 
     def logprobs(self, hidden: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -140,6 +144,7 @@ class RestrictedLMHead:
         head = _RowBlock(rows, id_t)
         if self.fp8:
             head.codes, head.scale = quantize_weight_fp8(rows)
+            head.pre = prearrange_fp8_weight(head.codes.t())
         self._head = head
         self._levels = []
 
