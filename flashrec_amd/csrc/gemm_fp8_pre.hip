@@ -67,6 +67,24 @@ __global__ __launch_bounds__(256) void fp8_weight_prearrange(const uint8_t* __re
   *reinterpret_cast<u32x4*>(out + 16 * c) = v;
 }
 
+// Tile order of a multi-round launch: XCD x (workgroups i with i % 8 == x)
+// owns the n-tiles [x * tilesN / 8, (x + 1) * tilesN / 8) over all m-tiles,
+// walked m-major, so its weight slice (3 MB at the config-1 shape) is what
+// every round of that XCD re-reads from its L2 while the activation panels
+// stream.  Single-round launches (and n-tile counts that do not split over 8
+// XCDs) keep the m-grouped order of tile_coords.
+__device__ __forceinline__ void tile_coords_pre(int64_t pid, int64_t nt, int64_t tilesM, bool multi_round,
+                                                int64_t& tm, int64_t& tn) {
+  const int64_t tilesN = nt / tilesM;
+  if (multi_round && (tilesN & 7) == 0) {
+    const int64_t x = pid & 7, p = pid >> 3, nper = tilesN >> 3;
+    tn = x * nper + p % nper;
+    tm = p / nper;
+    return;
+  }
+  tile_coords(pid, nt, tilesM, tm, tn);
+}
+
 // BN: weight rows (output columns) per tile, BM: activation rows, NSL: ring
 // slots, KTAIL: K % 128 != 0 (activation chunks past K read as zero).
 template <int BN, int BM, int NSL, int OUT, bool KTAIL, int EPI>
@@ -104,6 +122,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_pre(GemmArgs g) {
   const int64_t nt = tilesN * tilesM;
   const int64_t G = gridDim.x;
   const int64_t my_tiles = (nt - blockIdx.x + G - 1) / G;
+  const bool multi_round = nt > G && (G & 7) == 0;
   // K steps per tile: the prearranged layout's (a multiple of 4, >= K / 64)
   const uint32_t wblk = static_cast<uint32_t>(g.ldb);  // bytes per 32-row weight block
   const int KT = static_cast<int>(wblk / kPreBlockBytes);
@@ -132,7 +151,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_pre(GemmArgs g) {
       return;
     }
     int64_t tm, tn;
-    tile_coords(blockIdx.x + local * G, nt, tilesM, tm, tn);
+    tile_coords_pre(blockIdx.x + local * G, nt, tilesM, multi_round, tm, tn);
     ba = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(tm * BM * g.lda));
     wv = static_cast<uint32_t>((tn * (BN / 32) + wave * FN) * wblk) + 16 * lane_id_here();
   };
@@ -186,7 +205,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_pre(GemmArgs g) {
   auto load_scales = [&](int64_t local) __attribute__((always_inline)) {
     if (local >= my_tiles) return;
     int64_t tm, tn;
-    tile_coords(blockIdx.x + local * G, nt, tilesM, tm, tn);
+    tile_coords_pre(blockIdx.x + local * G, nt, tilesM, multi_round, tm, tn);
     uint8_t* dst = scl + (local & 1) * 2048;
     const uint32_t l16 = 16 * lane_id_here();
     if (wave == 0 && sb_vec)
@@ -197,7 +216,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_pre(GemmArgs g) {
   };
   auto epilogue = [&](int64_t local) __attribute__((always_inline)) {
     int64_t tm, tn;
-    tile_coords(blockIdx.x + local * G, nt, tilesM, tm, tn);
+    tile_coords_pre(blockIdx.x + local * G, nt, tilesM, multi_round, tm, tn);
     gemm_epilogue<BN, BM, WN, WM, OUT, EPI, SRB>(g, acc, tm, tn, wn, wm, scl + (local & 1) * 2048, stg, sa_vec,
                                                  sb_vec, sa0, sb0);
   };
