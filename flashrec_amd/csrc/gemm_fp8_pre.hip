@@ -35,7 +35,6 @@ namespace fr {
 
 constexpr int kPreBlockBytes = 2048;  // 32 rows x 64 bytes of K
 constexpr int kPreSteps = 4;          // K steps per prearranged group (KT is a multiple)
-constexpr int kPreWSets = 4;          // weight register sets (loads run 3 steps ahead)
 
 // KT for a K: 64-byte steps, rounded up to a multiple of kPreSteps.
 inline int64_t pre_k_steps(int64_t K) { return ((K + 64 * kPreSteps - 1) / (64 * kPreSteps)) * kPreSteps; }
@@ -87,7 +86,7 @@ __device__ __forceinline__ void tile_coords_pre(int64_t pid, int64_t nt, int64_t
 
 // BN: weight rows (output columns) per tile, BM: activation rows, NSL: ring
 // slots, KTAIL: K % 128 != 0 (activation chunks past K read as zero).
-template <int BN, int BM, int NSL, int OUT, bool KTAIL, int EPI>
+template <int BN, int BM, int NSL, int OUT, bool KTAIL, int EPI, int WS>
 __global__ __launch_bounds__(256, 1) void gemm_fp8_pre(GemmArgs g) {
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int RB = 128;        // bytes of K per LDS row: two MFMA steps per slot
@@ -165,7 +164,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_pre(GemmArgs g) {
   };
 
   // ---- weight registers: wr[set][block][half]
-  u32x4 wr[kPreWSets][FN][2];
+  u32x4 wr[WS][FN][2];
   // load `l` (block l / 2, half l % 2) of K step kt of the cur / nxt tile
   auto issue_w = [&](int set, int kt, bool next, int l) __attribute__((always_inline)) {
     const int i = l >> 1, h = l & 1;
@@ -248,7 +247,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_pre(GemmArgs g) {
       idx += IA;
       last_of[q] = idx - 1;
     }
-    idx += 3 * WL;
+    idx += (WS - 1) * WL;
     int best = 1 << 30;
     for (int st = 0; st < S; ++st) {
       const bool lst = st & 1;
@@ -283,10 +282,10 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_pre(GemmArgs g) {
     const int lq = lq0 < KS ? lq0 : lq0 - KS;
     const bool lnx = lq0 >= KS;
     // weights of step s + 3
-    const int wk0 = kt + 3;
+    const int wk0 = kt + WS - 1;
     const int wk = wk0 < KT ? wk0 : wk0 - KT;
     const bool wnx = wk0 >= KT;
-    const int wset = (set + 3) & 3;
+    const int wset = (set + WS - 1) % WS;
     if (last) lds_barrier();
 #pragma unroll
     for (int u = 0; u < NMF; ++u) {
@@ -324,26 +323,24 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_pre(GemmArgs g) {
 #pragma unroll
     for (int a = 0; a < IA; ++a) issue_a(st, st < KS ? st : st - KS, st >= KS, a);
 #pragma unroll
-  for (int st = 0; st < 3; ++st)
+  for (int st = 0; st < WS - 1; ++st)
 #pragma unroll
     for (int l = 0; l < WL; ++l) issue_w(st, st < KT ? st : st - KT, st >= KT, l);
-  waitcnt_vm<(NSL - 1) * IA + 3 * WL>();
+  waitcnt_vm<((NSL - 1) * IA + (WS - 1) * WL < 63 ? (NSL - 1) * IA + (WS - 1) * WL : 63)>();
   lds_barrier();
 #pragma unroll
   for (int j = 0; j < FM; ++j) read_a(0, 0, j);
 
+  // steps run in groups of WS (KT is a multiple of WS), so step s uses weight
+  // set s % WS and loads set (s + WS - 1) % WS, both known at compile time
   int64_t s = 0;
   for (int64_t tile = 0; tile < my_tiles; ++tile) {
-    step(0, s, 0, true);
-    step(1, s + 1, 1, false);
-    step(2, s + 2, 2, false);
-    step(3, s + 3, 3, false);
-    s += 4;
-    for (int kt = 4; kt < KT; kt += 4, s += 4) {
-      step(0, s, kt, false);
-      step(1, s + 1, kt + 1, false);
-      step(2, s + 2, kt + 2, false);
-      step(3, s + 3, kt + 3, false);
+#pragma unroll
+    for (int u = 0; u < WS; ++u) step(u, s + u, u, u == 0);
+    s += WS;
+    for (int kt = WS; kt < KT; kt += WS, s += WS) {
+#pragma unroll
+      for (int u = 0; u < WS; ++u) step(u, s + u, kt + u, false);
     }
     // the tile's scales (a direct-to-LDS load issued before its first step,
     // with KT * WL weight loads behind it) have landed
@@ -375,10 +372,13 @@ static hipError_t launch_pre(const GemmArgs& g, hipStream_t st) {
   // steps past K (K not a multiple of the 256-byte step group) must read
   // zero activations: the weights there are zero, but a stray e4m3 NaN
   // would still poison the sum
+  // four weight register sets (loads 3 steps ahead); eight on the smaller
+  // tiles, whose steps are half as long, measured 2-5 % slower on the down
+  // and o shapes
   if (g.K % (64 * kPreSteps) == 0)
-    hipLaunchKernelGGL((gemm_fp8_pre<BN, BM, NSL, OUT, false, EPI>), dim3(grid), dim3(256), 0, st, g);
+    hipLaunchKernelGGL((gemm_fp8_pre<BN, BM, NSL, OUT, false, EPI, 4>), dim3(grid), dim3(256), 0, st, g);
   else
-    hipLaunchKernelGGL((gemm_fp8_pre<BN, BM, NSL, OUT, true, EPI>), dim3(grid), dim3(256), 0, st, g);
+    hipLaunchKernelGGL((gemm_fp8_pre<BN, BM, NSL, OUT, true, EPI, 4>), dim3(grid), dim3(256), 0, st, g);
   return hipGetLastError();
 }
 
