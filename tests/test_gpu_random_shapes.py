@@ -3,7 +3,8 @@
 * the W8A8 GEMM against the fp32 dequantised oracle (max-abs-normalised
   1e-2 on sampled rows), its bf16 output equal to its fp32 output rounded
   once, the residual variant bit-exact with the GEMM then the add, the
-  SiLU-and-mul variant bit-exact with the GEMM then ``silu_and_mul``;
+  SiLU-and-mul variant bit-exact with the GEMM then ``silu_and_mul``; the
+  same four through the prearranged-weight kernel, equal to the plain ones;
 * paged attention against the oracle (1e-2 of each row's max) and the
   quantizing variant bit-exact with attention then the per-token quant, with
   and without the plan, on random head ratios, prefix lengths (0, partial and
@@ -27,8 +28,9 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("seed", range(24))
 def test_random_gemm_variants(dev, seed):
-    from flashrec_amd.kernel.sglops import (fp8_scaled_mm, fp8_scaled_mm_residual, fp8_scaled_mm_silu,
-                                            interleave_gate_up, silu_and_mul)
+    from flashrec_amd.kernel.sglops import (fp8_scaled_mm, fp8_scaled_mm_prearranged, fp8_scaled_mm_residual,
+                                            fp8_scaled_mm_silu, interleave_gate_up, prearrange_fp8_weight,
+                                            silu_and_mul)
 
     rnd = random.Random(seed)
     m = rnd.choice([1, 7, 33, 300, 512, 777, 1381, 2661, 4196])
@@ -49,6 +51,18 @@ def test_random_gemm_variants(dev, seed):
     assert torch.equal(got.cpu().view(torch.int16), want.view(torch.int16))
     got = fp8_scaled_mm_silu(a, interleave_gate_up(w).t(), s_a, interleave_gate_up(s_w))
     assert torch.equal(got.cpu().view(torch.int16), silu_and_mul(out16).cpu().view(torch.int16))
+    # prearranged weights: the same values (a zero K step may turn -0 into +0)
+    print(f"random gemm seed {seed}: {m}x{n}x{k}", flush=True)
+    pre = prearrange_fp8_weight(w.t())
+    assert torch.equal(fp8_scaled_mm_prearranged(a, pre, s_a, s_w, torch.float32).cpu(), out32.cpu())
+    assert torch.equal(fp8_scaled_mm_prearranged(a, pre, s_a, s_w, torch.bfloat16).cpu().float(),
+                       out16.cpu().float())
+    res2 = (torch.randn(m, n, generator=g) * 2).to(torch.bfloat16)
+    got = fp8_scaled_mm_prearranged(a, pre, s_a, s_w, residual=res2.to(dev))
+    assert torch.equal(got.cpu().float(), (res2 + out16.cpu()).float())
+    got = fp8_scaled_mm_prearranged(a, prearrange_fp8_weight(interleave_gate_up(w).t()), s_a,
+                                    interleave_gate_up(s_w), silu=True)
+    assert torch.equal(got.cpu().float(), silu_and_mul(out16).cpu().float())
 
 
 @pytest.mark.parametrize("seed", range(16))
