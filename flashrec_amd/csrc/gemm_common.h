@@ -237,7 +237,8 @@ __device__ __forceinline__ void tile_coords(int64_t pid, int64_t nt, int64_t til
 // written to a per-wave staging tile of 32 rows x SRB bytes per pass
 // (16-byte chunks XOR-swizzled by row), read back as 16 consecutive bytes
 // per lane and stored as whole SRB-byte row segments.  The tile's scales
-// were brought into LDS (`scl`: sb[BN] then sa[BM] as fp32) by direct loads
+// were brought into LDS (`scl`: sb[BN], then sa[BM] from the next 1 KB
+// boundary, as fp32) by direct loads
 // when the tile started, so the epilogue issues no global load (a load here
 // would queue behind the next tile's ring loads: vmcnt retires in order)
 // and holds no scale registers through the K loop.  Returns whether a fast
@@ -331,7 +332,8 @@ __device__ __forceinline__ bool gemm_epilogue(const GemmArgs& g, v16f (&acc)[WN 
   const int row = lx & 31;
   const int h4 = 4 * (lx >> 5);
   const uint32_t sbl = lds_addr(scl) + 4 * (wn * WN + h4);
-  const uint32_t sal = lds_addr(scl + 1024) + 4 * (wm * WM + row);
+  // sa[] follows sb[] at the next 1 KB boundary
+  const uint32_t sal = lds_addr(scl + ((BN * 4 + 1023) / 1024) * 1024) + 4 * (wm * WM + row);
   // Passes of 32 rows x SRB bytes: pass t = (column group cg, block row j),
   // cg outer, covering CPP output columns (NQ groups u of 8: lane l holds
   // columns 8u + 4(l/32) .. +3 of its row l%32).  The converted outputs go

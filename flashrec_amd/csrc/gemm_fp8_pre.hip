@@ -105,11 +105,14 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_pre(GemmArgs g) {
   static_assert(FN >= 1 && FM >= 1 && BN % 128 == 0 && BM % 32 == 0, "tile shape");
   static_assert(NSL >= 3, "the slot waits below assume at least three slots");
   constexpr int kLds = 160 * 1024;
-  constexpr bool kNarrow = NSL * STAGE + 2 * 2048 + 4 * 32 * 128 > kLds || WN % (128 / EB) != 0;
+  // scale buffer per tile parity: sb[BN], then sa[BM] from the next 1 KB
+  constexpr int SBB = (BN * 4 + 1023) / 1024, SAB = (BM * 4 + 1023) / 1024;  // 1 KB loads of each
+  constexpr int SCB = 1024 * (SBB + SAB);
+  constexpr bool kNarrow = NSL * STAGE + 2 * SCB + 4 * 32 * 128 > kLds || WN % (128 / EB) != 0;
   constexpr int SRB = kNarrow ? 64 : 128;
   constexpr int STG = 32 * SRB;
-  static_assert(NSL * STAGE + 2 * 2048 + 4 * STG <= kLds, "LDS");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[NSL * STAGE + 2 * 2048 + 4 * STG];
+  static_assert(NSL * STAGE + 2 * SCB + 4 * STG <= kLds, "LDS");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NSL * STAGE + 2 * SCB + 4 * STG];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -197,7 +200,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_pre(GemmArgs g) {
 
   // ---- scales and epilogue (shared with gemm_fp8.hip)
   uint8_t* const scl = smem + NSL * STAGE;
-  uint8_t* const stg = smem + NSL * STAGE + 2 * 2048 + wave * STG;
+  uint8_t* const stg = smem + NSL * STAGE + 2 * SCB + wave * STG;
   const bool sa_vec = g.sa_stride != 0, sb_vec = g.sb_stride != 0;
   const float sa0 = sa_vec ? 0.0f : __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(g.sa[0])));
   const float sb0 = sb_vec ? 0.0f : __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(g.sb[0])));
@@ -205,18 +208,24 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_pre(GemmArgs g) {
     if (local >= my_tiles) return;
     int64_t tm, tn;
     tile_coords_pre(blockIdx.x + local * G, nt, tilesM, multi_round, tm, tn);
-    uint8_t* dst = scl + (local & 1) * 2048;
+    uint8_t* dst = scl + (local & 1) * SCB;
     const uint32_t l16 = 16 * lane_id_here();
-    if (wave == 0 && sb_vec)
-      lds_dma_b128(g.sb, static_cast<uint32_t>(g.N * 4), lds_addr(dst), static_cast<uint32_t>(tn * BN * 4) + l16);
-    if (wave == 1 && sa_vec)
-      lds_dma_b128(g.sa, static_cast<uint32_t>(g.M * 4), lds_addr(dst + 1024),
-                   static_cast<uint32_t>(tm * BM * 4) + l16);
+    // 1 KB chunks: sb's on waves 0, 2, ..., sa's on waves 1, 3, ...
+#pragma unroll
+    for (int c = 0; c < SBB; ++c)
+      if (wave == (2 * c) % 4 && sb_vec)
+        lds_dma_b128(g.sb, static_cast<uint32_t>(g.N * 4), lds_addr(dst + 1024 * c),
+                     static_cast<uint32_t>(tn * BN * 4 + 1024 * c) + l16);
+#pragma unroll
+    for (int c = 0; c < SAB; ++c)
+      if (wave == (2 * c + 1) % 4 && sa_vec)
+        lds_dma_b128(g.sa, static_cast<uint32_t>(g.M * 4), lds_addr(dst + 1024 * (SBB + c)),
+                     static_cast<uint32_t>(tm * BM * 4 + 1024 * c) + l16);
   };
   auto epilogue = [&](int64_t local) __attribute__((always_inline)) {
     int64_t tm, tn;
     tile_coords_pre(blockIdx.x + local * G, nt, tilesM, multi_round, tm, tn);
-    gemm_epilogue<BN, BM, WN, WM, OUT, EPI, SRB>(g, acc, tm, tn, wn, wm, scl + (local & 1) * 2048, stg, sa_vec,
+    gemm_epilogue<BN, BM, WN, WM, OUT, EPI, SRB>(g, acc, tm, tn, wn, wm, scl + (local & 1) * SCB, stg, sa_vec,
                                                  sb_vec, sa0, sb0);
   };
 
@@ -361,7 +370,8 @@ template <int BN, int BM, int OUT, int EPI>
 static hipError_t launch_pre(const GemmArgs& g, hipStream_t st) {
   constexpr int RB = 128;
   constexpr int stage = BM * RB;
-  constexpr int fit = (160 * 1024 - 2 * 2048 - 4 * 32 * 128) / stage;
+  constexpr int scb = 1024 * ((BN * 4 + 1023) / 1024 + (BM * 4 + 1023) / 1024);
+  constexpr int fit = (160 * 1024 - 2 * scb - 4 * 32 * 128) / stage;
   constexpr int NSL = fit > 4 ? 4 : fit;
   const int64_t nt = ((g.N + BN - 1) / BN) * ((g.M + BM - 1) / BM);
   const int64_t cus = num_cus();
