@@ -397,8 +397,8 @@ static hipError_t launch_pre(const GemmArgs& g, hipStream_t st) {
 // MFMA work over its relative efficiency, measured with each tile forced
 // (operands rotated through HBM): 256x256 1.0; 256x128 0.75 (the down and o
 // projections: 2218-2243 and 1553-1738 TFLOP/s against 1506-1605 and
-// 1225-1267 on 256x256 tiles, which leave half the CUs idle there); 128x256
-// 0.7 and 128x128 0.6 (slower than 256x128 on every shape measured).
+// 1225-1267 on 256x256 tiles, which leave half the CUs idle there); 128x128
+// 0.6 (slower than 256x128 on every shape measured; taken by small launches).
 template <int OUT, int EPI>
 static hipError_t dispatch_pre(const GemmArgs& g, hipStream_t st) {
   const int64_t cus = num_cus();
@@ -406,11 +406,9 @@ static hipError_t dispatch_pre(const GemmArgs& g, hipStream_t st) {
     const int64_t tiles = ((g.N + bn - 1) / bn) * ((g.M + bm - 1) / bm);
     return static_cast<double>((tiles + cus - 1) / cus) * bn * bm / eff;
   };
-  const double c0 = cost(256, 256, 1.0), c1 = cost(256, 128, 0.75), c2 = cost(128, 256, 0.7),
-               c3 = cost(128, 128, 0.6);
-  if (c0 <= c1 && c0 <= c2 && c0 <= c3) return launch_pre<256, 256, OUT, EPI>(g, st);
-  if (c1 <= c2 && c1 <= c3) return launch_pre<256, 128, OUT, EPI>(g, st);
-  if (c2 <= c3) return launch_pre<128, 256, OUT, EPI>(g, st);
+  const double c0 = cost(256, 256, 1.0), c1 = cost(256, 128, 0.75), c3 = cost(128, 128, 0.6);
+  if (c0 <= c1 && c0 <= c3) return launch_pre<256, 256, OUT, EPI>(g, st);
+  if (c1 <= c3) return launch_pre<256, 128, OUT, EPI>(g, st);
   return launch_pre<128, 128, OUT, EPI>(g, st);
 }
 
