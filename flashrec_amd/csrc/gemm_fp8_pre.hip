@@ -248,7 +248,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_pre(GemmArgs g) {
   // the slot waited for, over the prologue and the first steps (the stream
   // is periodic from there; epilogue stores between tiles only add ops and
   // make the wait more conservative), found by replaying the issue order
-  constexpr int kWaitN = [] {
+  constexpr int kWaitN = [w_at, a_at] {
     constexpr int S = 2 * NSL + 24;
     int last_of[S / 2 + NSL + 2] = {};
     int idx = 0;
@@ -266,10 +266,10 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_pre(GemmArgs g) {
           best = c < best ? c : best;
         }
         for (int l = 0; l < WL; ++l)
-          if (l * NMF / WL == u) ++idx;
+          if (w_at(l) == u) ++idx;
         if (lst)
           for (int i = 0; i < IA; ++i)
-            if (i * NMF / IA == u) {
+            if (a_at(i) == u) {
               ++idx;
               if (i == IA - 1) last_of[st / 2 + NSL] = idx - 1;
             }
