@@ -29,6 +29,7 @@
 //    activation-block-major; each activation block's next-step fragment is
 //    read from LDS right after its last MFMA of the step (one register set).
 //  * Weights: 4 register sets; step s issues the loads of step s + 3.
+//  * Multi-round launches give each XCD a slice of n-tiles, walked m-major.
 #include "gemm_common.h"
 
 namespace fr {
@@ -68,9 +69,10 @@ __global__ __launch_bounds__(256) void fp8_weight_prearrange(const uint8_t* __re
 
 // Tile order of a multi-round launch: XCD x (workgroups i with i % 8 == x)
 // owns the n-tiles [x * tilesN / 8, (x + 1) * tilesN / 8) over all m-tiles,
-// walked m-major, so its weight slice (3 MB at the config-1 shape) is what
-// every round of that XCD re-reads from its L2 while the activation panels
-// stream.  Single-round launches (and n-tile counts that do not split over 8
+// walked m-major, so every round of that XCD revisits one weight slice (3 MB
+// at the config-1 shape) while the activation panels stream past (1-6 %
+// faster than the m-grouped order on the multi-round shapes measured).
+// Single-round launches (and n-tile counts that do not split over 8
 // XCDs) keep the m-grouped order of tile_coords.
 __device__ __forceinline__ void tile_coords_pre(int64_t pid, int64_t nt, int64_t tilesM, bool multi_round,
                                                 int64_t& tm, int64_t& tn) {
@@ -85,7 +87,9 @@ __device__ __forceinline__ void tile_coords_pre(int64_t pid, int64_t nt, int64_t
 }
 
 // BN: weight rows (output columns) per tile, BM: activation rows, NSL: ring
-// slots, KTAIL: K % 128 != 0 (activation chunks past K read as zero).
+// slots, KTAIL: K % 256 != 0 (activation chunks past K read as zero: the
+// prearranged K steps come in groups of 4), EPI: epilogue variant, WS: weight
+// register sets (step s loads step s + WS - 1's weights).
 template <int BN, int BM, int NSL, int OUT, bool KTAIL, int EPI, int WS>
 __global__ __launch_bounds__(256, 1) void gemm_fp8_pre(GemmArgs g) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -230,9 +234,9 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_pre(GemmArgs g) {
   };
 
   // ---- step schedule.  Step s (K step kt of its tile, ring slot s / 2,
-  // weight set s % 4).  Unit u = j * FN + i: MFMA (i, j), then, if it was
+  // weight set s % WS).  Unit u = j * FN + i: MFMA (i, j), then, if it was
   // block j's last, block j's next-step activation reads; the step's share
-  // of the weight loads of step s + 3 and, on a slot's second step, of the
+  // of the weight loads of step s + WS - 1 and, on a slot's second step, of the
   // slot's refill.  The second step of a slot opens with a barrier (every
   // wave is done reading the slot, which may then be refilled with the slot
   // NSL ahead) and at unit MW waits for the next slot (own loads, then a
