@@ -294,7 +294,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_pre(GemmArgs g) {
     const int lq0 = kt / 2 + NSL;
     const int lq = lq0 < KS ? lq0 : lq0 - KS;
     const bool lnx = lq0 >= KS;
-    // weights of step s + 3
+    // weights of step s + WS - 1
     const int wk0 = kt + WS - 1;
     const int wk = wk0 < KT ? wk0 : wk0 - KT;
     const bool wnx = wk0 >= KT;
